@@ -1,0 +1,171 @@
+#!/usr/bin/env python3
+"""Write the golden input/output vectors for every quant type.
+
+Runs ONLY in the build container, where the reference checkout is mounted at
+/root/reference. It imports the reference's per-type modules (kernels/*.py) and
+calls their eager CPU quantizers (the path `--device cpu` takes:
+quant-studio.py:216-232 -> quant_fn) on seeded synthetic inputs, then stores
+inputs and outputs as small .npz fixtures next to this script. Nothing from the
+reference is stored except its outputs.
+
+The reference imports gguf-py only for enum names (kernels/common.py:6-7,
+kernels/q4_0.py:6-7, ...). gguf-py is not installed here, so this script
+provides a minimal stand-in module exposing those names with the public GGUF
+enum values; no arithmetic depends on it.
+
+Usage: python tests/golden/gen_golden.py [--ref /root/reference]
+"""
+
+from __future__ import annotations
+
+import argparse
+import enum
+import sys
+import types
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+
+# public ggml type ids and llama file types (GGUF spec); names only matter here
+GGML_TYPES = dict(F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, Q5_1=7, Q8_0=8, Q8_1=9, Q2_K=10,
+                  Q3_K=11, Q4_K=12, Q5_K=13, Q6_K=14, Q8_K=15, IQ2_XXS=16, IQ2_XS=17,
+                  IQ3_XXS=18, IQ1_S=19, IQ4_NL=20, IQ3_S=21, IQ2_S=22, IQ4_XS=23, I8=24,
+                  I16=25, I32=26, I64=27, F64=28, IQ1_M=29, BF16=30, TQ1_0=34, TQ2_0=35,
+                  MXFP4=39)
+FILE_TYPES = dict(ALL_F32=0, MOSTLY_F16=1, MOSTLY_Q4_0=2, MOSTLY_Q4_1=3, MOSTLY_Q8_0=7,
+                  MOSTLY_Q5_0=8, MOSTLY_Q5_1=9, MOSTLY_Q2_K=10, MOSTLY_Q3_K_S=11,
+                  MOSTLY_Q3_K_M=12, MOSTLY_Q3_K_L=13, MOSTLY_Q4_K_S=14, MOSTLY_Q4_K_M=15,
+                  MOSTLY_Q5_K_S=16, MOSTLY_Q5_K_M=17, MOSTLY_Q6_K=18, MOSTLY_IQ2_XXS=19,
+                  MOSTLY_IQ2_XS=20, MOSTLY_Q2_K_S=21, MOSTLY_IQ3_XS=22, MOSTLY_IQ3_XXS=23,
+                  MOSTLY_IQ1_S=24, MOSTLY_IQ4_NL=25, MOSTLY_IQ3_S=26, MOSTLY_IQ3_M=27,
+                  MOSTLY_IQ2_S=28, MOSTLY_IQ2_M=29, MOSTLY_IQ4_XS=30, MOSTLY_IQ1_M=31,
+                  MOSTLY_BF16=32, MOSTLY_TQ1_0=36, MOSTLY_TQ2_0=37, MOSTLY_MXFP4_MOE=38)
+
+
+def install_enum_module() -> None:
+    g = types.ModuleType("gguf")
+    c = types.ModuleType("gguf.constants")
+    g.GGMLQuantizationType = enum.IntEnum("GGMLQuantizationType", GGML_TYPES)
+    c.LlamaFileType = enum.IntEnum("LlamaFileType", FILE_TYPES)
+    g.LlamaFileType = c.LlamaFileType
+    g.GGML_QUANT_VERSION = 2
+    g.constants = c
+    sys.modules["gguf"] = g
+    sys.modules["gguf.constants"] = c
+
+
+# (type name, reference module, function, imatrix modes)
+TYPES = [
+    ("q4_0", "q4_0", "quantize_q4_0", ("none",)),
+    ("q2_k", "q2_k", "quantize_q2_k", ("none", "imat")),
+    ("q3_k", "q3_k", "quantize_q3_k", ("none", "imat")),
+    ("q4_k", "q4_k", "quantize_q4_k", ("none", "imat")),
+    ("q5_k", "q5_k", "quantize_q5_k", ("none", "imat")),
+    ("q6_k", "q6_k", "quantize_q6_k", ("none", "imat")),
+    ("iq4_xs", "iq4_xs", "quantize_iq4_xs", ("none", "imat")),
+    ("iq2_xxs", "iq2", "quantize_iq2_xxs", ("imat",)),
+    ("iq2_xs", "iq2_xs", "quantize_iq2_xs", ("imat",)),
+    ("iq2_s", "iq2_s", "quantize_iq2_s", ("imat",)),
+    ("iq3_xxs", "iq3_xxs", "quantize_iq3_xxs", ("imat",)),
+    ("iq3_s", "iq3_s", "quantize_iq3_s", ("none", "imat")),
+]
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """f32 -> bf16 bit patterns (round to nearest even), as uint16."""
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def make_cases() -> dict[str, dict[str, np.ndarray]]:
+    """Seeded inputs. bf16 cases store bf16 bits; the f32 case stores raw f32."""
+    cases = {}
+    rng = np.random.default_rng(20261201)
+
+    # adversarial rows modelled on the reference's synthetic model (zeros, constants,
+    # an outlier over tiny values, half-constant, one-signed rows) plus scale extremes
+    k = 1024
+    a = rng.standard_normal((16, k)) * 0.05 * (0.2 + rng.random((16, 1)) * 3.0)
+    a[0, :] = 0.0
+    a[1, :] = 0.5
+    a[2, :] = -0.5
+    a[3, :] = 1e-6
+    a[3, 7] = 8.0
+    a[4, :128] = 0.25
+    a[5, :] = np.abs(a[5, :])
+    a[6, :] = -np.abs(a[6, :])
+    a[7, :] = rng.standard_normal(k) * 1e-17          # below the 1e-15 dead-group threshold
+    a[8, :] = rng.standard_normal(k) * 1e-9           # between 1e-15 and 1e-8
+    a[9, :] = rng.standard_normal(k) * 300.0
+    a[10, ::2] = 0.0                                  # sparse row
+    a[11, :] = np.round(rng.standard_normal(k) * 4) / 64.0   # coarse lattice values: many ties
+    a[12, :256] = 0.0
+    a[12, 3] = -1e-3
+    a[13, :] = np.where(rng.random(k) < 0.5, 0.02, -0.02)
+    cases["synth"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
+
+    # C2-like: N(0, 0.02) with log-normal per-row std jitter, 0.1% outliers x20
+    rows, k = 64, 512
+    a = rng.standard_normal((rows, k)) * 0.02 * np.exp(0.3 * rng.standard_normal((rows, 1)))
+    idx = rng.choice(rows * k, rows * k // 1000, replace=False)
+    a.reshape(-1)[idx] *= 20.0
+    cases["normal"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
+
+    # C4-like: Student-t df=5 scaled to std 0.02
+    rows, k = 32, 512
+    a = rng.standard_t(5, (rows, k)) * 0.02 / np.sqrt(5.0 / 3.0)
+    cases["student"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
+
+    # raw f32 input (not bf16-representable) for the F32 source path
+    rows, k = 8, 512
+    a = (rng.standard_normal((rows, k)) * 0.05).astype(np.float32)
+    cases["f32"] = dict(x=a, imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
+    return cases
+
+
+def case_f32(case: dict[str, np.ndarray]) -> np.ndarray:
+    x = case["x"]
+    return bf16_to_f32(x) if x.dtype == np.uint16 else x
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--ref", default="/root/reference")
+    ap.add_argument("--out", default=str(HERE))
+    args = ap.parse_args()
+
+    install_enum_module()
+    sys.path.insert(0, args.ref)
+    import importlib
+
+    torch.set_num_threads(1)
+    cases = make_cases()
+    inputs = {}
+    for cname, c in cases.items():
+        inputs[f"{cname}.x"] = c["x"]
+        inputs[f"{cname}.imat"] = c["imat"]
+    np.savez_compressed(Path(args.out) / "inputs.npz", **inputs)
+
+    for tname, mod, fn, modes in TYPES:
+        m = importlib.import_module(f"kernels.{mod}")
+        f = getattr(m, fn)
+        outs = {}
+        for cname, c in cases.items():
+            x = torch.from_numpy(case_f32(c).copy())
+            for mode in modes:
+                qw = torch.from_numpy(c["imat"].copy()) if mode == "imat" else None
+                y = f(x) if tname == "q4_0" else f(x, qw)
+                outs[f"{cname}.{mode}"] = y.numpy().astype(np.uint8)
+        np.savez_compressed(Path(args.out) / f"{tname}.npz", **outs)
+        print(f"{tname}: {', '.join(f'{k}={v.shape}' for k, v in outs.items())}", flush=True)
+
+
+if __name__ == "__main__":
+    main()
