@@ -1,0 +1,47 @@
+/*
+ * CPU oracle for the GGUF block quantizers -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's eager CPU path (the kernels/ modules run
+ * under torch on CPU), used by the tests as the parity checker and by the
+ * benchmark as the timed CPU baseline. The product path never links, loads or
+ * calls it.
+ *
+ * Every function cites the reference file:line it follows. All arithmetic is
+ * IEEE f32 with one rounding per torch op (built with -ffp-contract=off); the
+ * reduction orders reproduce what torch 2.10's CPU kernels do for the sums
+ * the reference writes (`.sum(-1)`, tree_sum, seq_sum).
+ */
+#ifndef QS_ORACLE_H
+#define QS_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids (GGUF spec) */
+enum {
+    QSO_Q4_0 = 2, QSO_Q2_K = 10, QSO_Q3_K = 11, QSO_Q4_K = 12, QSO_Q5_K = 13,
+    QSO_Q6_K = 14, QSO_IQ2_XXS = 16, QSO_IQ2_XS = 17, QSO_IQ3_XXS = 18,
+    QSO_IQ3_S = 21, QSO_IQ2_S = 22, QSO_IQ4_XS = 23
+};
+
+/* bytes of one quantized row of k elements, or -1 for an unsupported type / k */
+int64_t qso_row_bytes(int ggml_type, int64_t k);
+
+/* Quantize x (n_rows x k, row-major f32) into out (n_rows * row_bytes bytes).
+ * qw: k per-column imatrix weights or NULL. Returns 0, or -1 on bad arguments. */
+int qso_quantize(int ggml_type, const float *x, int64_t n_rows, int64_t k,
+                 const float *qw, uint8_t *out, int n_threads);
+
+/* Sum helpers exposed for the tests that pin them against torch. */
+float qso_sum_cascade8(const float *v, int n);
+float qso_sum_tree(const float *v, int n);
+uint16_t qso_f32_to_f16(float f);
+float qso_f16_to_f32(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
