@@ -1,0 +1,96 @@
+/*
+ * quant_studio.h -- C ABI of the MI355X (gfx950) GGUF block quantizer library
+ * (libqs_hip.so). Plain pointers and sizes only; no torch or HIP types in the
+ * signatures (the stream is passed as an opaque hipStream_t value).
+ *
+ * The reference's plugin interface for this path is the QuantSpec registry:
+ *   QuantSpec(ggml_type, ftype, bytes_per_elem, needs_imatrix, make_kernel,
+ *             uses_imatrix)                       kernels/common.py:27-37
+ *   make_kernel(device, qw) -> quant_fn           e.g. kernels/q4_k.py:82-83
+ *   quant_fn(x: f32 (n, k)) -> uint8 (n, k//blk*type_size)
+ *                                                 e.g. kernels/q4_k.py:25-27
+ * called once per row chunk by the pipeline (quant-studio.py:198 on the GPU,
+ * :229 on the CPU). qs_quantize() replaces one quant_fn call; the imatrix
+ * argument is make_kernel's qw; the bf16/f16 source is read in-kernel, which
+ * replaces the pipeline's separate upcast pass (quant-studio.py:197).
+ *
+ * Return codes: 0 on success, a negative errno-style value on failure
+ * (QS_EINVAL, QS_ENOTSUP, QS_EIO); qs_last_error() then describes it.
+ */
+#ifndef QUANT_STUDIO_H
+#define QUANT_STUDIO_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QS_ABI_VERSION 1
+
+#define QS_EINVAL (-22)
+#define QS_ENOTSUP (-95)
+#define QS_EIO (-5)
+
+/* ggml type ids (GGUF spec) accepted as ggml_type */
+#define QS_TYPE_Q4_0 2
+#define QS_TYPE_Q2_K 10
+#define QS_TYPE_Q3_K 11
+#define QS_TYPE_Q4_K 12
+#define QS_TYPE_Q5_K 13
+#define QS_TYPE_Q6_K 14
+#define QS_TYPE_IQ2_XXS 16
+#define QS_TYPE_IQ2_XS 17
+#define QS_TYPE_IQ3_XXS 18
+#define QS_TYPE_IQ3_S 21
+#define QS_TYPE_IQ2_S 22
+#define QS_TYPE_IQ4_XS 23
+
+/* source element types accepted as src_type (ggml ids; TORCH_DTYPES
+ * kernels/common.py:20-24) */
+#define QS_SRC_F32 0
+#define QS_SRC_F16 1
+#define QS_SRC_BF16 30
+
+/* Version of this ABI (QS_ABI_VERSION). */
+int qs_abi_version(void);
+
+/* 1 if ggml_type has a HIP quantizer in this build, else 0. Mirrors the
+ * registry membership test `type in QUANT_TYPES` (kernels/__init__.py:18-27,
+ * quant-studio.py:396-399). */
+int qs_type_supported(int ggml_type);
+
+/* 1 if the type cannot run without an imatrix (QuantSpec.needs_imatrix,
+ * kernels/common.py:33), 0 if not, QS_ENOTSUP for an unknown type. */
+int qs_type_needs_imatrix(int ggml_type);
+
+/* 1 if the type uses an imatrix when one is given (QuantSpec.uses_imatrix,
+ * kernels/common.py:36; Q4_0 ignores it, q4_0.py:36-37). */
+int qs_type_uses_imatrix(int ggml_type);
+
+/* Bytes of one quantized row of k values (k/blk * type_size, the BLOCK_BYTES
+ * constants e.g. kernels/q4_k.py:19), or QS_EINVAL if k is not a multiple of
+ * the block size (the precondition of every quant_fn, e.g. q4_k.py:26). */
+int64_t qs_row_bytes(int ggml_type, int64_t k);
+
+/* Quantize n_rows rows of k values (one quant_fn call, e.g. q4_k.py:25-79).
+ *   src:           device pointer to the first row; 16-byte aligned
+ *   src_row_stride_bytes: distance between rows, a multiple of 16, >= k*elem
+ *   imatrix:       device pointer to k f32 column weights, or NULL; required
+ *                  when qs_type_needs_imatrix(); ignored by Q4_0
+ *   dst:           device pointer receiving n_rows * qs_row_bytes(k) bytes;
+ *                  dst_bytes must be at least that
+ *   hip_stream:    hipStream_t to launch on (NULL = null stream)
+ * Asynchronous and stream-ordered; allocates nothing. The output bytes do not
+ * depend on how rows are split across calls. */
+int qs_quantize(int ggml_type, int src_type, const void *src, int64_t n_rows, int64_t k,
+                int64_t src_row_stride_bytes, const float *imatrix, void *dst,
+                int64_t dst_bytes, void *hip_stream);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char *qs_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QUANT_STUDIO_H */

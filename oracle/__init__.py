@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.qso_sum_tree.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.qso_f32_to_f16.restype = ctypes.c_uint16
         L.qso_f32_to_f16.argtypes = [ctypes.c_float]
+        L.qso_set_mutation.restype = None
+        L.qso_set_mutation.argtypes = [ctypes.c_int]
         _lib = L
     return _lib
 

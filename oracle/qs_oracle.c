@@ -24,8 +24,20 @@
 #define GROUP_MAX_EPS 1e-15f
 #define F32_TINY 1.17549435e-38f
 
+/* Planted-mistake switch for the tests that show the golden vectors pin each
+ * convention (0 = the faithful restatement). */
+static int g_mut = 0;
+void qso_set_mutation(int m) { g_mut = m; }
+enum { MUT_IEEE_RDIV = 1, MUT_SEQ_CASCADE = 2, MUT_SEQ_TREE = 3, MUT_DROP_STEP = 4,
+       MUT_ROUND_AWAY = 5, MUT_ACCEPT_GE = 6 };
+
 /* torch: python_float / tensor  ->  tensor.reciprocal() * python_float */
-static inline float RDIV(float c, float t) { float r = 1.0f / t; return r * c; }
+static inline float RDIV(float c, float t) {
+    if (g_mut == MUT_IEEE_RDIV) return c / t;
+    float r = 1.0f / t;
+    return r * c;
+}
+static inline float RINT(float v) { return g_mut == MUT_ROUND_AWAY ? roundf(v) : rintf(v); }
 static inline float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
 /* ------------------------------------------------------------------ */
@@ -85,6 +97,11 @@ static inline float f16_round(float v) { return qso_f16_to_f32(qso_f32_to_f16(v)
  * fed round-robin, leftover vectors into accumulator 0, accumulators combined
  * ((a0+a1)+a2)+a3, then a scalar pass over the tail and the 8 lanes. */
 float qso_sum_cascade8(const float *v, int n) {
+    if (g_mut == MUT_SEQ_CASCADE) {
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += v[i];
+        return s;
+    }
     int nv = n / 8, full = nv / 4;
     float acc[4][8];
     for (int a = 0; a < 4; a++)
@@ -107,6 +124,11 @@ float qso_sum_cascade8(const float *v, int n) {
 
 /* tree_sum kq_common.py:38-43 (twins iq2xs_common.py:33-38, iq3_common.py:71-75) */
 float qso_sum_tree(const float *v, int n) {
+    if (g_mut == MUT_SEQ_TREE) {
+        float s = v[0];
+        for (int i = 1; i < n; i++) s += v[i];
+        return s;
+    }
     float t[256];
     for (int i = 0; i < n; i++) t[i] = v[i];
     for (int m = n; m > 1; m >>= 1)
@@ -186,7 +208,7 @@ static void make_qkx(const float *x, const float *w, int n, const float *steps, 
     float den = degen ? 1.0f : mx - mn;
     float iscale = fmax / den;
     float scale = 1.0f / iscale;
-    for (int i = 0; i < n; i++) L[i] = clampf(rintf(iscale * (x[i] - mn)), 0.0f, fmax);
+    for (int i = 0; i < n; i++) L[i] = clampf(RINT(iscale * (x[i] - mn)), 0.0f, fmax);
     for (int i = 0; i < n; i++) {
         float d = scale * L[i];
         d = d + mn;
@@ -195,12 +217,13 @@ static void make_qkx(const float *x, const float *w, int n, const float *steps, 
     }
     float best = qso_sum_tree(tmp, n);
 
+    if (g_mut == MUT_DROP_STEP) nsteps--;
     for (int s = 0; s < nsteps; s++) {
         den = degen ? 1.0f : mx - mn;
         float isc = steps[s] / den;
         float wl[32], t2[32], t3[32];
         for (int i = 0; i < n; i++) {
-            Laux[i] = clampf(rintf(isc * (x[i] - mn)), 0.0f, fmax);
+            Laux[i] = clampf(RINT(isc * (x[i] - mn)), 0.0f, fmax);
             wl[i] = w[i] * Laux[i];
             t2[i] = wl[i] * Laux[i];
             t3[i] = wl[i] * x[i];
@@ -258,7 +281,7 @@ static void make_qp(const float *x, const float *w, int n, int nmax, int f64_ste
 
     float iscale = RDIV(fmax, mxs);
     for (int i = 0; i < n; i++) {
-        float l0 = rintf(iscale * x[i]);                 /* first pass: no clamp */
+        float l0 = RINT(iscale * x[i]);                 /* first pass: no clamp */
         float r = (1.0f / iscale) * l0;
         float d = x[i] - r;
         tmp[i] = w[i] * (d * d);
@@ -268,14 +291,14 @@ static void make_qp(const float *x, const float *w, int n, int nmax, int f64_ste
         float isc = RDIV(steps[s], mxs);
         float ri = 1.0f / isc;
         for (int i = 0; i < n; i++) {
-            float l = fminf(rintf(isc * x[i]), fmax);
+            float l = fminf(RINT(isc * x[i]), fmax);
             float d = x[i] - ri * l;
             tmp[i] = w[i] * (d * d);
         }
         float mse = qso_sum_cascade8(tmp, n);
         if (mse < best_mse) { best_mse = mse; iscale = isc; }
     }
-    for (int i = 0; i < n; i++) L[i] = fminf(rintf(iscale * x[i]), fmax);
+    for (int i = 0; i < n; i++) L[i] = fminf(RINT(iscale * x[i]), fmax);
     float t2[32];
     for (int i = 0; i < n; i++) { tmp[i] = (w[i] * x[i]) * L[i]; t2[i] = (w[i] * L[i]) * L[i]; }
     float sumlx = qso_sum_cascade8(tmp, n), suml2 = qso_sum_cascade8(t2, n);
@@ -285,7 +308,7 @@ static void make_qp(const float *x, const float *w, int n, int nmax, int f64_ste
             float slx = sumlx - (wi * xi) * Li;
             float sl2 = suml2 - (wi * Li) * Li;
             int ok = slx > 0 && sl2 > 0;
-            float newl = fminf(rintf((xi * sl2) / (ok ? slx : 1.0f)), fmax);
+            float newl = fminf(RINT((xi * sl2) / (ok ? slx : 1.0f)), fmax);
             float slx2 = slx + (wi * xi) * newl;
             float sl22 = sl2 + (wi * newl) * newl;
             if (ok && newl != Li && (slx2 * slx2) * suml2 > (sumlx * sumlx) * sl22) {
@@ -314,7 +337,7 @@ static void make_qx(const float *x, const float *w, int n, int nmax, float *scal
     qx_steps(nmax, steps);
 
     float iscale = RDIV(-fmax, mxs);
-    for (int i = 0; i < n; i++) L[i] = clampf(rintf(iscale * x[i]), -fmax, fmax - 1.0f);
+    for (int i = 0; i < n; i++) L[i] = clampf(RINT(iscale * x[i]), -fmax, fmax - 1.0f);
     for (int i = 0; i < n; i++) { tmp[i] = (w[i] * x[i]) * L[i]; t2[i] = (w[i] * L[i]) * L[i]; }
     float sumlx = sum_seq(tmp, n), suml2 = sum_seq(t2, n);
     float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
@@ -322,12 +345,12 @@ static void make_qx(const float *x, const float *w, int n, int nmax, float *scal
     for (int s = 0; s < 18; s++) {
         float isc = RDIV(-steps[s], mxs);
         for (int i = 0; i < n; i++) {
-            La[i] = clampf(rintf(isc * x[i]), -fmax, fmax - 1.0f);
+            La[i] = clampf(RINT(isc * x[i]), -fmax, fmax - 1.0f);
             tmp[i] = (w[i] * x[i]) * La[i];
             t2[i] = (w[i] * La[i]) * La[i];
         }
         float slx = sum_seq(tmp, n), sl2 = sum_seq(t2, n);
-        if (sl2 > 0 && slx * slx > best * sl2) {
+        if (sl2 > 0 && (g_mut == MUT_ACCEPT_GE ? slx * slx >= best * sl2 : slx * slx > best * sl2)) {
             float cand = slx / sl2;
             scale = cand;
             best = cand * slx;
@@ -347,7 +370,7 @@ static void make_q3(const float *x, int n, int nmax, float *scale_out, float *Lo
     int live = amax >= GROUP_MAX_EPS;
     float mxs = live ? mx : 1.0f;
     float iscale = RDIV(-fmax, mxs);
-    for (int i = 0; i < n; i++) L[i] = clampf(rintf(iscale * x[i]), -fmax, fmax - 1.0f);
+    for (int i = 0; i < n; i++) L[i] = clampf(RINT(iscale * x[i]), -fmax, fmax - 1.0f);
     for (int i = 0; i < n; i++) { tmp[i] = (w[i] * x[i]) * L[i]; t2[i] = (w[i] * L[i]) * L[i]; }
     float sumlx = sum_seq(tmp, n), suml2 = sum_seq(t2, n);
     for (int pass = 0; pass < 5; pass++) {
@@ -356,7 +379,7 @@ static void make_q3(const float *x, int n, int nmax, float *scale_out, float *Lo
             float slx = sumlx - (wi * xi) * Li;
             int ok = slx > 0;
             float sl2 = suml2 - (wi * Li) * Li;
-            float newl = clampf(rintf((xi * sl2) / (ok ? slx : 1.0f)), -fmax, fmax - 1.0f);
+            float newl = clampf(RINT((xi * sl2) / (ok ? slx : 1.0f)), -fmax, fmax - 1.0f);
             float slx2 = slx + (wi * xi) * newl;
             float sl22 = sl2 + (wi * newl) * newl;
             if (ok && newl != Li && sl22 > 0 && (slx2 * slx2) * suml2 > (sumlx * sumlx) * sl22) {
@@ -423,8 +446,8 @@ static void q2_k_block(const float *x, const float *qw, uint8_t *out) {
         float inv_s = pos_s ? 15.0f / max_scale : 0.0f;
         float inv_m = pos_m ? 15.0f / max_min : 0.0f;
         for (int g = 0; g < 16; g++) {
-            ls[g] = (int64_t)rintf(inv_s * sc[g]) & 0xFF;
-            lm[g] = (int64_t)rintf(inv_m * mn[g]) & 0xFF;
+            ls[g] = (int64_t)RINT(inv_s * sc[g]) & 0xFF;
+            lm[g] = (int64_t)RINT(inv_m * mn[g]) & 0xFF;
         }
         d16 = f16_round(pos_s ? max_scale / 15.0f : 0.0f);
         m16 = f16_round(pos_m ? max_min / 15.0f : 0.0f);
@@ -452,7 +475,7 @@ static void q2_k_block(const float *x, const float *qw, uint8_t *out) {
             float v;
             if (dg != 0) {
                 float t = x[16 * g + i] + mg;
-                v = clampf(rintf(t / dg), 0.0f, 3.0f);
+                v = clampf(RINT(t / dg), 0.0f, 3.0f);
             } else v = L[16 * g + i];
             Lf[16 * g + i] = (int)v;
         }
@@ -480,7 +503,7 @@ static void q3_k_block(const float *x, const float *qw, uint8_t *out) {
         int has = max_scale != 0;
         float iscale = RDIV(-32.0f, has ? max_scale : 1.0f);
         for (int g = 0; g < 16; g++) {
-            int64_t l = (int64_t)rintf(iscale * sc[g]);
+            int64_t l = (int64_t)RINT(iscale * sc[g]);
             l = ((l & 0xFF) ^ 0x80) - 0x80;
             l = l < -32 ? -32 : (l > 31 ? 31 : l);
             ls6[g] = has ? l + 32 : 0;
@@ -504,7 +527,7 @@ static void q3_k_block(const float *x, const float *qw, uint8_t *out) {
         float dq = d16 * (float)(ls6[g] - 32);
         for (int i = 0; i < 16; i++) {
             float v;
-            if (dq != 0) v = clampf(rintf(x[16 * g + i] / dq), -4.0f, 3.0f) + 4.0f;
+            if (dq != 0) v = clampf(RINT(x[16 * g + i] / dq), -4.0f, 3.0f) + 4.0f;
             else v = L[16 * g + i];
             Lf[16 * g + i] = (int)v;
         }
@@ -550,7 +573,7 @@ static void q45_k_block(const float *x, const float *qw, uint8_t *out, int nmax)
         float inv_s = max_scale > 0 ? RDIV(63.0f, max_scale) : 0.0f;
         float inv_m = max_min > 0 ? RDIV(63.0f, max_min) : 0.0f;
         for (int g = 0; g < 8; g++) {
-            int64_t a = (int64_t)rintf(inv_s * sc[g]) & 0xFF, b = (int64_t)rintf(inv_m * mn[g]) & 0xFF;
+            int64_t a = (int64_t)RINT(inv_s * sc[g]) & 0xFF, b = (int64_t)RINT(inv_m * mn[g]) & 0xFF;
             ls[g] = a > 63 ? 63 : a;
             lm[g] = b > 63 ? 63 : b;
         }
@@ -578,7 +601,7 @@ static void q45_k_block(const float *x, const float *qw, uint8_t *out, int nmax)
             float v;
             if (dg != 0) {
                 float t = x[32 * g + i] + mg;
-                v = clampf(rintf(t / dg), 0.0f, (float)nmax);
+                v = clampf(RINT(t / dg), 0.0f, (float)nmax);
             } else v = L[32 * g + i];
             Lf[32 * g + i] = (int)v;
         }
@@ -622,12 +645,12 @@ static void q6_k_block(const float *x, const float *qw, uint8_t *out) {
     int64_t sc8[16];
     int Lf[QK_K];
     for (int g = 0; g < 16; g++) {
-        int64_t s = (int64_t)fminf(rintf(iscale * sc[g]), 127.0f);
+        int64_t s = (int64_t)fminf(RINT(iscale * sc[g]), 127.0f);
         s = ((s & 0xFF) ^ 0x80) - 0x80;
         float dq = d16 * (float)s;
         for (int i = 0; i < 16; i++) {
             float v;
-            if (dq != 0) v = clampf(rintf(x[16 * g + i] / dq), -32.0f, 31.0f) + 32.0f;
+            if (dq != 0) v = clampf(RINT(x[16 * g + i] / dq), -32.0f, 31.0f) + 32.0f;
             else v = L[16 * g + i];
             Lf[16 * g + i] = live ? (int)v : 0;
         }
@@ -705,7 +728,7 @@ static void iq4_xs_block(const float *x, const float *qw, uint8_t *out) {
     float idq = d != 0 ? 1.0f / d : 0.0f;
     int lsq[8], L[QK_K];
     for (int b = 0; b < 8; b++) {
-        float ls = clampf(rintf(idq * sc[b]), -32.0f, 31.0f);
+        float ls = clampf(RINT(idq * sc[b]), -32.0f, 31.0f);
         float dl = d * ls;
         float idl = dl != 0 ? 1.0f / dl : 0.0f;
         for (int i = 0; i < 32; i++) L[32 * b + i] = iq4_best_index(idl * x[32 * b + i]);

@@ -39,6 +39,8 @@ int qso_quantize(int ggml_type, const float *x, int64_t n_rows, int64_t k,
 float qso_sum_cascade8(const float *v, int n);
 float qso_sum_tree(const float *v, int n);
 uint16_t qso_f32_to_f16(float f);
+/* Test hook: plant a known mistake (1..6, see qs_oracle.c); 0 restores the oracle. */
+void qso_set_mutation(int m);
 float qso_f16_to_f32(uint16_t h);
 
 #ifdef __cplusplus

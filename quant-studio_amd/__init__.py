@@ -1,0 +1,183 @@
+"""MI355X-native GGUF block quantizers behind the reference's plugin API.
+
+Mirrors the reference's kernel registry (kernels/__init__.py:18-27,
+kernels/common.py:20-37): `QUANT_TYPES` maps a lowercase type name to a
+`QuantSpec`, whose `make_kernel(device, qw)` returns `quant_fn(x) -> uint8`.
+Here every quant_fn is one call into the gfx950 HIP library (libqs_hip.so,
+C ABI in include/quant_studio.h) on torch's current stream. There is no CPU
+path: the library must be built (build.py) and a ROCm device present, and
+every failure raises.
+
+Import with `importlib.import_module("quant-studio_amd")` (the directory name
+is not an identifier).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import sys
+from pathlib import Path
+
+import torch
+
+from .gguf_types import GGMLQuantizationType, LlamaFileType
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "_build" / "libqs_hip.so"
+
+F32_TINY = torch.finfo(torch.float32).tiny
+
+# source dtypes the quantizers read directly (kernels/common.py:20-24)
+TORCH_DTYPES = {
+    GGMLQuantizationType.F32: torch.float32,
+    GGMLQuantizationType.F16: torch.float16,
+    GGMLQuantizationType.BF16: torch.bfloat16,
+}
+_SRC_IDS = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 30}
+
+_lib: ctypes.CDLL | None = None
+
+
+class QuantSpecError(RuntimeError):
+    """A quantizer call was rejected or failed in the HIP library."""
+
+
+def library() -> ctypes.CDLL:
+    """Load libqs_hip.so (built in-tree by build.py); raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is missing: build it with "
+                              "quant-studio_amd/build.py (or __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.qs_abi_version.restype = ctypes.c_int
+        L.qs_type_supported.restype = ctypes.c_int
+        L.qs_type_supported.argtypes = [ctypes.c_int]
+        L.qs_type_needs_imatrix.restype = ctypes.c_int
+        L.qs_type_needs_imatrix.argtypes = [ctypes.c_int]
+        L.qs_type_uses_imatrix.restype = ctypes.c_int
+        L.qs_type_uses_imatrix.argtypes = [ctypes.c_int]
+        L.qs_row_bytes.restype = ctypes.c_int64
+        L.qs_row_bytes.argtypes = [ctypes.c_int, ctypes.c_int64]
+        L.qs_quantize.restype = ctypes.c_int
+        L.qs_quantize.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                  ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                  ctypes.c_int64, ctypes.c_void_p]
+        L.qs_last_error.restype = ctypes.c_char_p
+        if L.qs_abi_version() != 1:
+            raise ImportError(f"{LIB_PATH}: ABI version {L.qs_abi_version()} != 1")
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return library().qs_last_error().decode()
+
+
+def row_bytes(ggml_type: int, k: int) -> int:
+    rb = library().qs_row_bytes(int(ggml_type), int(k))
+    if rb < 0:
+        raise ValueError(last_error())
+    return rb
+
+
+def quantize(ggml_type: int, x: torch.Tensor, qw: torch.Tensor | None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """Quantize the rows of x (n, k) on its ROCm device; returns uint8 (n, row_bytes).
+
+    x: float32 / float16 / bfloat16, unit stride along k, 16-byte aligned rows.
+    qw: (k,) float32 imatrix column weights on the same device, or None.
+    The launch goes on torch's current stream; nothing is synchronised."""
+    if x.device.type != "cuda":
+        raise ValueError(f"quant_fn: x must be on a ROCm device, got {x.device}")
+    if x.dim() != 2:
+        raise ValueError(f"quant_fn: x must be 2-D (n, k), got shape {tuple(x.shape)}")
+    if x.dtype not in _SRC_IDS:
+        raise ValueError(f"quant_fn: unsupported dtype {x.dtype}")
+    n, k = x.shape
+    if x.stride(1) != 1 and k > 1:
+        x = x.contiguous()
+    rb = row_bytes(ggml_type, k)
+    if out is None:
+        out = torch.empty((n, rb), dtype=torch.uint8, device=x.device)
+    elif out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < n * rb:
+        raise ValueError("quant_fn: out must be contiguous uint8 with n*row_bytes elements")
+    qptr = None
+    if qw is not None:
+        if qw.device != x.device or qw.dtype != torch.float32 or qw.numel() < k:
+            raise ValueError("quant_fn: qw must be float32 with k values on x's device")
+        qw = qw.contiguous()
+        qptr = qw.data_ptr()
+    stride_bytes = (x.stride(0) if n > 1 else k) * x.element_size()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    rc = library().qs_quantize(int(ggml_type), _SRC_IDS[x.dtype], x.data_ptr(), n, k,
+                               stride_bytes, qptr, out.data_ptr(), out.numel(), stream)
+    if rc != 0:
+        raise QuantSpecError(last_error())
+    return out.view(n, rb) if out.dim() != 2 else out
+
+
+class QuantSpec:
+    """Same fields and meaning as the reference's QuantSpec (kernels/common.py:27-37)."""
+
+    def __init__(self, ggml_type: GGMLQuantizationType, ftype: LlamaFileType,
+                 bytes_per_elem: int, needs_imatrix: bool, make_kernel,
+                 uses_imatrix: bool | None = None):
+        self.ggml_type = ggml_type
+        self.ftype = ftype
+        self.bytes_per_elem = bytes_per_elem  # rough full-pipeline working set per element
+        self.needs_imatrix = needs_imatrix
+        self.make_kernel = make_kernel        # (device, qw_tensor|None) -> fn(x)->uint8
+        self.uses_imatrix = needs_imatrix if uses_imatrix is None else uses_imatrix
+
+
+def _kernel_factory(ggml_type: GGMLQuantizationType, uses_imatrix: bool):
+    def make_kernel(device: torch.device, qw):
+        q = qw if uses_imatrix else None    # Q4_0 ignores an imatrix (q4_0.py:36-37)
+        if q is not None:
+            q = q.to(device=device, dtype=torch.float32).contiguous()
+        return lambda x: quantize(ggml_type, x, q)
+    return make_kernel
+
+
+# (name, ggml type, file type, bytes_per_elem, needs_imatrix, uses_imatrix): the
+# SPECS entries of the reference modules (q4_0.py:40-43, q2_k.py:88-91,
+# q3_k.py:85-88, q4_k.py:86-89, q5_k.py:89-92, q6_k.py:72-75, iq4_xs.py:195-198,
+# iq2.py:506-509, iq2_xs.py:77-80, iq2_s.py:70-73, iq3_xxs.py:143-146,
+# iq3_s.py:148-151)
+_T, _F = GGMLQuantizationType, LlamaFileType
+_SPECS = [
+    ("q4_0", _T.Q4_0, _F.MOSTLY_Q4_0, 16, False, False),
+    ("q2_k", _T.Q2_K, _F.MOSTLY_Q2_K, 24, False, True),
+    ("q3_k", _T.Q3_K, _F.MOSTLY_Q3_K_M, 24, False, True),
+    ("q4_k", _T.Q4_K, _F.MOSTLY_Q4_K_M, 24, False, True),
+    ("q5_k", _T.Q5_K, _F.MOSTLY_Q5_K_M, 24, False, True),
+    ("q6_k", _T.Q6_K, _F.MOSTLY_Q6_K, 24, False, True),
+    ("iq4_xs", _T.IQ4_XS, _F.MOSTLY_IQ4_XS, 24, False, True),
+    ("iq2_xxs", _T.IQ2_XXS, _F.MOSTLY_IQ2_XXS, 64, True, True),
+    ("iq2_xs", _T.IQ2_XS, _F.MOSTLY_IQ2_XS, 64, True, True),
+    ("iq2_s", _T.IQ2_S, _F.MOSTLY_IQ2_S, 64, True, True),
+    ("iq3_xxs", _T.IQ3_XXS, _F.MOSTLY_IQ3_XXS, 64, True, True),
+    ("iq3_s", _T.IQ3_S, _F.MOSTLY_IQ3_S, 64, False, True),
+]
+ALL_SPECS: dict[str, QuantSpec] = {
+    name: QuantSpec(t, f, bpe, needs, _kernel_factory(t, uses), uses)
+    for name, t, f, bpe, needs, uses in _SPECS
+}
+
+
+def _registry() -> dict[str, QuantSpec]:
+    """Types with a HIP quantizer in the loaded library (registry semantics of
+    kernels/__init__.py:18-27: a type without a kernel is simply absent)."""
+    try:
+        L = library()
+    except ImportError as e:  # like a kernel module that fails to import: warn, register nothing
+        print(f"warning: quant-studio_amd: {e}", file=sys.stderr)
+        return {}
+    return {n: s for n, s in ALL_SPECS.items() if L.qs_type_supported(int(s.ggml_type))}
+
+
+QUANT_TYPES: dict[str, QuantSpec] = _registry()
+
+__all__ = ["QUANT_TYPES", "ALL_SPECS", "QuantSpec", "QuantSpecError", "TORCH_DTYPES",
+           "GGMLQuantizationType", "LlamaFileType", "library", "quantize", "row_bytes"]

@@ -1,0 +1,229 @@
+// C ABI of the gfx950 quantizer library: argument checks, per-type launch
+// geometry and template dispatch. Declarations and the reference interfaces
+// they replace are in include/quant_studio.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "quant_studio.h"
+#include "qs_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+struct TypeInfo {
+    int id;
+    const char* name;
+    int blk, bytes;
+    bool needs_imatrix, uses_imatrix;
+};
+
+// block sizes and type sizes: BLOCK_BYTES of each reference module
+// (q4_0.py:11/:30-32, q2_k.py:19, q3_k.py:20, q4_k.py:19, q5_k.py:19,
+// q6_k.py:19, iq4_xs.py:20, iq2.py:27, ...); imatrix flags from the SPECS
+// entries (q4_0.py:40-43, q2_k.py:88-91, ..., iq3_s.py:148-151).
+constexpr TypeInfo kTypes[] = {
+    {QS_TYPE_Q4_0, "q4_0", 32, 18, false, false},
+    {QS_TYPE_Q2_K, "q2_k", 256, 84, false, true},
+    {QS_TYPE_Q3_K, "q3_k", 256, 110, false, true},
+    {QS_TYPE_Q4_K, "q4_k", 256, 144, false, true},
+    {QS_TYPE_Q5_K, "q5_k", 256, 176, false, true},
+    {QS_TYPE_Q6_K, "q6_k", 256, 210, false, true},
+    {QS_TYPE_IQ4_XS, "iq4_xs", 256, 136, false, true},
+    {QS_TYPE_IQ2_XXS, "iq2_xxs", 256, 66, true, true},
+    {QS_TYPE_IQ2_XS, "iq2_xs", 256, 74, true, true},
+    {QS_TYPE_IQ2_S, "iq2_s", 256, 82, true, true},
+    {QS_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, true, true},
+    {QS_TYPE_IQ3_S, "iq3_s", 256, 110, false, true},
+};
+
+const TypeInfo* find_type(int id) {
+    for (const auto& t : kTypes)
+        if (t.id == id) return &t;
+    return nullptr;
+}
+
+bool has_kernel(int id) {
+    switch (id) {
+    case QS_TYPE_Q4_0: case QS_TYPE_Q2_K: case QS_TYPE_Q3_K: case QS_TYPE_Q4_K:
+    case QS_TYPE_Q5_K: case QS_TYPE_Q6_K: case QS_TYPE_IQ4_XS:
+        return true;
+    default:
+        return false;
+    }
+}
+
+// candidate numerators, f32 chains as kq_common.py:21-30 and qx_common.py:20-23
+qs::Steps qkx_steps(float rmin, float rdelta, int nstep, int nmax) {
+    qs::Steps s{};
+    for (int i = 0; i <= nstep; i++) {
+        float t = rdelta * (float)i;
+        t = rmin + t;
+        s.v[i] = t + (float)nmax;
+    }
+    s.n = nstep + 1;
+    return s;
+}
+
+qs::QpSteps qp_steps(int nmax) {
+    qs::QpSteps s{};
+    int n = 0;
+    for (int i = -4; i <= 4; i++) {
+        if (!i) continue;
+        float t = 0.1f * (float)i;
+        s.v[n++] = t + (float)nmax;
+    }
+    return s;
+}
+
+qs::Steps qx_steps(int nmax) {
+    qs::Steps s{};
+    int n = 0;
+    for (int i = -9; i <= 9; i++) {
+        if (!i) continue;
+        float t = 0.1f * (float)i;
+        s.v[n++] = (float)nmax + t;
+    }
+    s.n = n;
+    return s;
+}
+
+template <int SRC>
+void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st) {
+    using namespace qs;
+    const unsigned sb8 = (unsigned)((a.n_units + 7) / 8), sb4 = (unsigned)((a.n_units + 3) / 4);
+    switch (type) {
+    case QS_TYPE_Q4_0: {
+        const unsigned g = (unsigned)((a.n_units + Q40_BLOCKS_PER_WG - 1) / Q40_BLOCKS_PER_WG);
+        hipLaunchKernelGGL(k_q4_0<SRC>, dim3(g), dim3(256), 0, st, a);
+        break;
+    }
+    case QS_TYPE_Q4_K:
+        if (imat) hipLaunchKernelGGL((k_q45_k<SRC, true, 15>), dim3(sb8), dim3(64), 0, st, a,
+                                     qkx_steps(-0.9f, 0.05f, 36, 15), qp_steps(63));
+        else hipLaunchKernelGGL((k_q45_k<SRC, false, 15>), dim3(sb8), dim3(64), 0, st, a,
+                                qkx_steps(-1.0f, 0.1f, 20, 15), qp_steps(63));
+        break;
+    case QS_TYPE_Q5_K:
+        if (imat) hipLaunchKernelGGL((k_q45_k<SRC, true, 31>), dim3(sb8), dim3(64), 0, st, a,
+                                     qkx_steps(-0.9f, 0.05f, 36, 31), qp_steps(63));
+        else hipLaunchKernelGGL((k_q45_k<SRC, false, 31>), dim3(sb8), dim3(64), 0, st, a,
+                                qkx_steps(-0.5f, 0.1f, 15, 31), qp_steps(63));
+        break;
+    case QS_TYPE_Q6_K:
+        if (imat) hipLaunchKernelGGL((k_q6_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a, qx_steps(32));
+        else hipLaunchKernelGGL((k_q6_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a, qx_steps(32));
+        break;
+    case QS_TYPE_Q3_K:
+        if (imat) hipLaunchKernelGGL((k_q3_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a, qx_steps(4),
+                                     qx_steps(32));
+        else hipLaunchKernelGGL((k_q3_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a, qx_steps(4),
+                                qx_steps(32));
+        break;
+    case QS_TYPE_Q2_K:
+        if (imat) hipLaunchKernelGGL((k_q2_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a,
+                                     qkx_steps(-0.9f, 0.05f, 36, 3), qp_steps(15));
+        else hipLaunchKernelGGL((k_q2_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a,
+                                qkx_steps(-0.5f, 0.1f, 15, 3), qp_steps(15));
+        break;
+    case QS_TYPE_IQ4_XS:
+        if (imat) hipLaunchKernelGGL((k_iq4_xs<SRC, true>), dim3(sb8), dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((k_iq4_xs<SRC, false>), dim3(sb8), dim3(64), 0, st, a);
+        break;
+    default:
+        break;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int qs_abi_version(void) { return QS_ABI_VERSION; }
+
+int qs_type_supported(int ggml_type) { return has_kernel(ggml_type) ? 1 : 0; }
+
+int qs_type_needs_imatrix(int ggml_type) {
+    const TypeInfo* t = find_type(ggml_type);
+    if (!t) return fail(QS_ENOTSUP, "unknown ggml type %d", ggml_type);
+    return t->needs_imatrix ? 1 : 0;
+}
+
+int qs_type_uses_imatrix(int ggml_type) {
+    const TypeInfo* t = find_type(ggml_type);
+    if (!t) return fail(QS_ENOTSUP, "unknown ggml type %d", ggml_type);
+    return t->uses_imatrix ? 1 : 0;
+}
+
+int64_t qs_row_bytes(int ggml_type, int64_t k) {
+    const TypeInfo* t = find_type(ggml_type);
+    if (!t) return fail(QS_ENOTSUP, "unknown ggml type %d", ggml_type);
+    if (k <= 0 || k % t->blk)
+        return fail(QS_EINVAL, "%s: row length %lld is not a positive multiple of %d", t->name,
+                    (long long)k, t->blk);
+    return k / t->blk * t->bytes;
+}
+
+const char* qs_last_error(void) { return g_err.c_str(); }
+
+int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, int64_t k,
+                int64_t src_row_stride_bytes, const float* imatrix, void* dst, int64_t dst_bytes,
+                void* hip_stream) {
+    g_err.clear();
+    const TypeInfo* t = find_type(ggml_type);
+    if (!t) return fail(QS_ENOTSUP, "unknown ggml type %d", ggml_type);
+    if (!has_kernel(ggml_type)) return fail(QS_ENOTSUP, "%s: no HIP quantizer in this build", t->name);
+    const int esz = src_type == QS_SRC_F32 ? 4 : (src_type == QS_SRC_F16 || src_type == QS_SRC_BF16) ? 2 : 0;
+    if (!esz) return fail(QS_EINVAL, "unsupported source type %d (F32=0, F16=1, BF16=30)", src_type);
+    if (n_rows < 0) return fail(QS_EINVAL, "n_rows %lld < 0", (long long)n_rows);
+    if (k <= 0 || k % t->blk)
+        return fail(QS_EINVAL, "%s: row length %lld is not a positive multiple of %d", t->name,
+                    (long long)k, t->blk);
+    const int64_t rb = k / t->blk * t->bytes;
+    if (n_rows == 0) return 0;
+    if (!src || !dst) return fail(QS_EINVAL, "null src or dst");
+    if (src_row_stride_bytes < k * esz || src_row_stride_bytes % 16)
+        return fail(QS_EINVAL, "row stride %lld must be >= %lld and a multiple of 16",
+                    (long long)src_row_stride_bytes, (long long)(k * esz));
+    if (reinterpret_cast<uintptr_t>(src) % 16) return fail(QS_EINVAL, "src must be 16-byte aligned");
+    if (dst_bytes < n_rows * rb)
+        return fail(QS_EINVAL, "dst holds %lld bytes, %lld needed", (long long)dst_bytes,
+                    (long long)(n_rows * rb));
+    if (t->needs_imatrix && !imatrix) return fail(QS_EINVAL, "%s requires an imatrix", t->name);
+    const bool imat = t->uses_imatrix && imatrix != nullptr;
+
+    qs::KArgs a;
+    a.src = src;
+    a.units_per_row = k / t->blk;
+    a.n_units = n_rows * a.units_per_row;
+    a.stride = src_row_stride_bytes / esz;
+    a.qw = imat ? imatrix : nullptr;
+    a.dst = static_cast<uint8_t*>(dst);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    (void)hipGetLastError();
+    switch (src_type) {
+    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st); break;
+    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st); break;
+    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(QS_EIO, "%s: launch failed: %s", t->name, hipGetErrorString(e));
+    return 0;
+}
+
+}  // extern "C"

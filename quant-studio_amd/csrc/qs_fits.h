@@ -1,0 +1,353 @@
+// Per-group scale/min searches of the K-quants and IQ4_XS, one lane per group.
+//
+// Each function keeps a whole group (16 or 32 values) in registers and walks
+// the reference's sequential candidate chain for it; parallelism comes from
+// running one group per lane. The candidate order, the accept tests and every
+// reduction order follow the reference's eager torch path line by line (cited
+// per function), so the chosen levels and scales are bit-identical to it.
+#pragma once
+
+#include "qs_device.h"
+
+namespace qs {
+
+// Candidate numerators. Computed on the host in f32 exactly as the reference's
+// numpy f32 chains (kq_common.py:21-30, qx_common.py:20-23) and passed in.
+struct Steps {
+    float v[40];
+    int n;
+};
+
+// Result of the make_qkx2/qkx3 search: the levels are regenerated from
+// (isc, mn) of the accepted candidate instead of being carried in registers.
+struct QkxResult {
+    float scale, the_min, isc, mn;
+    bool degen;
+};
+
+// make_qkx_quants_eager kq_common.py:51-96 for one group of N values.
+template <int N, bool MAD>
+QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& steps, float fmax) {
+    float mn = x[0], mx = x[0];
+#pragma unroll
+    for (int i = 1; i < N; i++) {
+        mn = fminf(mn, x[i]);
+        mx = fmaxf(mx, x[i]);
+    }
+    mn = fminf(mn, 0.0f);
+    const bool degen = (mx == mn);
+    float t[N];
+    const float sum_w = tree_sum(w);
+#pragma unroll
+    for (int i = 0; i < N; i++) t[i] = w[i] * x[i];
+    const float sum_x = tree_sum(t);
+
+    float den = degen ? 1.0f : mx - mn;
+    const float iscale = fmax / den;
+    float scale = 1.0f / iscale;
+    float best_isc = iscale, best_mn = mn;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        float L = clampf(rintf(iscale * (x[i] - mn)), 0.0f, fmax);
+        float d = scale * L;
+        d = d + mn;
+        d = d - x[i];
+        t[i] = w[i] * (MAD ? fabsf(d) : d * d);
+    }
+    float best = tree_sum(t);
+
+#pragma unroll 1
+    for (int s = 0; s < steps.n; s++) {
+        den = degen ? 1.0f : mx - mn;
+        const float isc = steps.v[s] / den;
+        float La[N], a[N], b[N], c[N];
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            La[i] = clampf(rintf(isc * (x[i] - mn)), 0.0f, fmax);
+            a[i] = w[i] * La[i];
+            b[i] = a[i] * La[i];
+            c[i] = a[i] * x[i];
+        }
+        const float sum_l = tree_sum(a), sum_l2 = tree_sum(b), sum_xl = tree_sum(c);
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        const float Dsafe = D > 0 ? D : 1.0f;
+        float this_scale = (sum_w * sum_xl - sum_x * sum_l) / Dsafe;
+        float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / Dsafe;
+        if (this_min > 0) {
+            this_scale = sum_xl / fmaxf(sum_l2, F32_TINY);
+            this_min = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            float d = this_scale * La[i];
+            d = d + this_min;
+            d = d - x[i];
+            t[i] = w[i] * (MAD ? fabsf(d) : d * d);
+        }
+        const float cur = tree_sum(t);
+        if (D > 0 && cur < best && !degen) {
+            best_isc = isc;
+            best_mn = mn;
+            scale = this_scale;
+            mn = this_min;
+            best = cur;
+        }
+    }
+    QkxResult r;
+    r.scale = degen ? 0.0f : scale;
+    r.the_min = (mn == 0.0f) ? 0.0f : -mn;
+    r.isc = best_isc;
+    r.mn = best_mn;
+    r.degen = degen;
+    return r;
+}
+
+// level i of the accepted make_qkx candidate
+QS_DEV float qkx_level(const QkxResult& r, float x, float fmax) {
+    return r.degen ? 0.0f : clampf(rintf(r.isc * (x - r.mn)), 0.0f, fmax);
+}
+
+// make_qp_quants_eager kq_common.py:99-141 for N sub-block scales (N = 8, 16).
+// Writes the levels to L and returns the scale.
+template <int N>
+QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const float (&steps)[8], float (&L)[N]) {
+    const float fmax = (float)nmax;
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < N; i++) mx = fmaxf(mx, x[i]);
+    const bool dead = mx < GROUP_MAX_EPS;
+    const float mxs = dead ? 1.0f : mx;
+    float t[N];
+
+    float iscale = rdiv(fmax, mxs);
+    {
+        const float r = 1.0f / iscale;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            float l0 = rintf(iscale * x[i]);
+            float d = x[i] - r * l0;
+            t[i] = w[i] * (d * d);
+        }
+    }
+    float best_mse = cascade8_sum(t);
+#pragma unroll 1
+    for (int s = 0; s < 8; s++) {
+        const float isc = rdiv(steps[s], mxs);
+        const float r = 1.0f / isc;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            float l = fminf(rintf(isc * x[i]), fmax);
+            float d = x[i] - r * l;
+            t[i] = w[i] * (d * d);
+        }
+        const float mse = cascade8_sum(t);
+        if (mse < best_mse) {
+            best_mse = mse;
+            iscale = isc;
+        }
+    }
+    float u[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        L[i] = fminf(rintf(iscale * x[i]), fmax);
+        t[i] = (w[i] * x[i]) * L[i];
+        u[i] = (w[i] * L[i]) * L[i];
+    }
+    float sumlx = cascade8_sum(t), suml2 = cascade8_sum(u);
+#pragma unroll 1
+    for (int pass = 0; pass < 5; pass++) {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const float xi = x[i], wi = w[i], Li = L[i];
+            const float slx = sumlx - (wi * xi) * Li;
+            const float sl2 = suml2 - (wi * Li) * Li;
+            const bool ok = slx > 0 && sl2 > 0;
+            const float newl = fminf(rintf((xi * sl2) / (ok ? slx : 1.0f)), fmax);
+            const float slx2 = slx + (wi * xi) * newl;
+            const float sl22 = sl2 + (wi * newl) * newl;
+            if (ok && newl != Li && (slx2 * slx2) * suml2 > (sumlx * sumlx) * sl22) {
+                L[i] = newl;
+                sumlx = slx2;
+                suml2 = sl22;
+            }
+        }
+    }
+    float scale = suml2 > 0 ? sumlx / fmaxf(suml2, F32_TINY) : 0.0f;
+    if (dead) {
+        scale = 0.0f;
+#pragma unroll
+        for (int i = 0; i < N; i++) L[i] = 0.0f;
+    }
+    return scale;
+}
+
+// make_qx_quants_eager qx_common.py:52-82 for one group of 16 values.
+// Returns the scale; the levels are regenerated from (isc) by qx_level.
+struct QxResult {
+    float scale, isc;
+    bool live;
+};
+
+template <int N>
+QS_DEV QxResult qx_fit(const float (&x)[N], const float (&w)[N], int nmax, const Steps& steps) {
+    const float fmax = (float)nmax;
+    float amax;
+    const float mx = absmax_first(x, amax);
+    const bool live = amax >= GROUP_MAX_EPS;
+    const float mxs = live ? mx : 1.0f;
+    float t[N], u[N];
+    const float iscale = rdiv(-fmax, mxs);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        float L = clampf(rintf(iscale * x[i]), -fmax, fmax - 1.0f);
+        t[i] = (w[i] * x[i]) * L;
+        u[i] = (w[i] * L) * L;
+    }
+    const float sumlx = seq_sum(t), suml2 = seq_sum(u);
+    float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx, best_isc = iscale;
+#pragma unroll 1
+    for (int s = 0; s < steps.n; s++) {
+        const float isc = rdiv(-steps.v[s], mxs);
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            float La = clampf(rintf(isc * x[i]), -fmax, fmax - 1.0f);
+            t[i] = (w[i] * x[i]) * La;
+            u[i] = (w[i] * La) * La;
+        }
+        const float slx = seq_sum(t), sl2 = seq_sum(u);
+        if (sl2 > 0 && slx * slx > best * sl2) {
+            const float cand = slx / sl2;
+            scale = cand;
+            best = cand * slx;
+            best_isc = isc;
+        }
+    }
+    QxResult r;
+    r.scale = live ? scale : 0.0f;
+    r.isc = best_isc;
+    r.live = live;
+    return r;
+}
+
+// level (0 .. 2*nmax-1) of the accepted make_qx candidate
+QS_DEV float qx_level(const QxResult& r, float x, float fmax) {
+    return r.live ? clampf(rintf(r.isc * x), -fmax, fmax - 1.0f) + fmax : 0.0f;
+}
+
+// make_q3_quants_eager qx_common.py:85-121 for one group of 16 (w = x*x).
+// Writes levels (0 .. 2*nmax-1) and returns the scale.
+template <int N>
+QS_DEV float q3_fit(const float (&x)[N], int nmax, float (&L)[N]) {
+    const float fmax = (float)nmax;
+    float w[N], t[N], u[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = x[i] * x[i];
+    float amax;
+    const float mx = absmax_first(x, amax);
+    const bool live = amax >= GROUP_MAX_EPS;
+    const float mxs = live ? mx : 1.0f;
+    const float iscale = rdiv(-fmax, mxs);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        L[i] = clampf(rintf(iscale * x[i]), -fmax, fmax - 1.0f);
+        t[i] = (w[i] * x[i]) * L[i];
+        u[i] = (w[i] * L[i]) * L[i];
+    }
+    float sumlx = seq_sum(t), suml2 = seq_sum(u);
+#pragma unroll 1
+    for (int pass = 0; pass < 5; pass++) {
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const float xi = x[i], wi = w[i], Li = L[i];
+            const float slx = sumlx - (wi * xi) * Li;
+            const bool ok = slx > 0;
+            const float sl2 = suml2 - (wi * Li) * Li;
+            const float newl = clampf(rintf((xi * sl2) / (ok ? slx : 1.0f)), -fmax, fmax - 1.0f);
+            const float slx2 = slx + (wi * xi) * newl;
+            const float sl22 = sl2 + (wi * newl) * newl;
+            if (ok && newl != Li && sl22 > 0 && (slx2 * slx2) * suml2 > (sumlx * sumlx) * sl22) {
+                L[i] = newl;
+                sumlx = slx2;
+                suml2 = sl22;
+            }
+        }
+    }
+    const float scale = suml2 > 0 ? sumlx / suml2 : 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; i++) L[i] = live ? L[i] + fmax : 0.0f;
+    return live ? scale : 0.0f;
+}
+
+// ---- IQ4_XS (iq4_xs.py:23-76) ----
+
+// best_index_int8 iq4_xs.py:35-39: count LUT entries <= al (searchsorted
+// right), clamp to 1..15, then the strict midpoint compare.
+QS_DEV int iq4_index(float al) {
+    constexpr float V[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                             1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+    int mu = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mu += (V[i] <= al) ? 1 : 0;
+    mu = mu < 1 ? 1 : (mu > 15 ? 15 : mu);
+    // lo = V[mu-1], hi = V[mu] without dynamic register indexing
+    float lo = V[0], hi = V[1];
+#pragma unroll
+    for (int i = 2; i < 16; i++) {
+        bool sel = (mu == i);
+        lo = sel ? V[i - 1] : lo;
+        hi = sel ? V[i] : hi;
+    }
+    return (al - lo < hi - al) ? mu - 1 : mu;
+}
+
+QS_DEV float iq4_value(int idx) {
+    constexpr float V[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                             1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+    float v = V[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) v = (idx == i) ? V[i] : v;
+    return v;
+}
+
+// _search_scales_eager iq4_xs.py:52-76 for one block of 32
+QS_DEV float iq4_scale_search(const float (&x)[32], const float (&w)[32]) {
+    float amax;
+    const float mx = absmax_first(x, amax);
+    const bool live = fabsf(mx) >= GROUP_MAX_EPS;
+    const float mxs = live ? mx : 1.0f;
+    const float d0 = -mxs / -127.0f;
+    const float id0 = 1.0f / d0;
+    float t[32], u[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float q = iq4_value(iq4_index(id0 * x[i]));
+        float wq = w[i] * q;
+        t[i] = wq * x[i];
+        u[i] = wq * q;
+    }
+    float sumqx = seq_sum(t), sumq2 = seq_sum(u);
+    float d = sumq2 > 0 ? sumqx / sumq2 : 0.0f;
+    float best = d * sumqx;
+#pragma unroll 1
+    for (int itry = -7; itry <= 7; itry++) {
+        const float idv = rdiv((float)(itry - 127), mxs);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            float q = iq4_value(iq4_index(idv * x[i]));
+            float wq = w[i] * q;
+            t[i] = wq * x[i];
+            u[i] = wq * q;
+        }
+        sumqx = seq_sum(t);
+        sumq2 = seq_sum(u);
+        if (sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            const float nd = sumqx / sumq2;
+            d = nd;
+            best = nd * sumqx;
+        }
+    }
+    return live ? d : 0.0f;
+}
+
+}  // namespace qs

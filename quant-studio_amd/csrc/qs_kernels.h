@@ -1,0 +1,616 @@
+// Quantizer kernels for Q4_0, Q2_K..Q6_K and IQ4_XS on gfx950.
+//
+// Q4_0 is HBM-bound: four lanes per 32-value block, 16-byte coalesced loads,
+// a cross-lane first-index absmax, output staged through LDS and stored with
+// coalesced dwords.
+//
+// The K-quants and IQ4_XS are VALU-bound (their scale searches cost hundreds of
+// f32 ops per value): one lane per 16/32-value group keeps the group and its
+// sequential candidate chain in registers, one 64-lane workgroup covers 4 or 8
+// superblocks, and the superblock-level steps (sums over 256 values, the
+// sub-scale fits) exchange data through LDS.
+#pragma once
+
+#include "qs_fits.h"
+#include "qs_wave.h"
+
+namespace qs {
+
+struct KArgs {
+    const void* src;      // source rows (F32 / F16 / BF16)
+    int64_t n_units;      // superblocks (or Q4_0 blocks)
+    int64_t units_per_row;
+    int64_t stride;       // source row stride in elements
+    const float* qw;      // k imatrix weights or nullptr
+    uint8_t* dst;         // packed output, n_units * block bytes
+};
+
+struct QpSteps {
+    float v[8];
+};
+
+// ------------------------------------------------------------------
+// Q4_0  (q4_0.py:14-33)
+// ------------------------------------------------------------------
+constexpr int Q40_BLOCKS_PER_WG = 64;  // 256 threads, 4 lanes per block
+
+template <int SRC>
+__global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t stage[Q40_BLOCKS_PER_WG * 18];
+    const int tid = threadIdx.x;
+    const int q = tid & 3;                       // quarter of the block: values 8q..8q+7
+    const int64_t b0 = (int64_t)blockIdx.x * Q40_BLOCKS_PER_WG;
+    int64_t b = b0 + (tid >> 2);
+    const bool valid = b < a.n_units;
+    b = valid ? b : a.n_units - 1;
+    const int64_t row = b / a.units_per_row;
+    const int64_t col = (b % a.units_per_row) * 32 + 8 * q;
+    float x[8];
+    load_elems<SRC, true, 8>(a.src, row * a.stride + col, x);
+
+    // signed value of the largest |x|, first index wins (argmax of abs)
+    float am = fabsf(x[0]), mv = x[0];
+    int idx = 8 * q;
+#pragma unroll
+    for (int i = 1; i < 8; i++) {
+        const float v = fabsf(x[i]);
+        const bool gt = v > am;
+        am = gt ? v : am;
+        mv = gt ? x[i] : mv;
+        idx = gt ? 8 * q + i : idx;
+    }
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+        const float pam = __shfl_xor(am, m, 4);
+        const float pmv = __shfl_xor(mv, m, 4);
+        const int pidx = __shfl_xor(idx, m, 4);
+        const bool take = pam > am || (pam == am && pidx < idx);
+        am = take ? pam : am;
+        mv = take ? pmv : mv;
+        idx = take ? pidx : idx;
+    }
+    const float d = mv / -8.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t nib = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float t = x[i] * id;
+        t = t + 8.5f;
+        const uint32_t qv = (uint32_t)clampf(floorf(t), 0.0f, 15.0f);
+        nib |= qv << (4 * i);
+    }
+    // qs[j] = q[j] | q[j+16] << 4: quarters 0/1 take the high nibbles of 2/3
+    const uint32_t hi = __shfl_xor(nib, 2, 4);
+    uint8_t* o = stage + (tid >> 2) * 18;
+    if (q == 0) {
+        const uint32_t h = f16_bits(d);
+        o[0] = (uint8_t)h;
+        o[1] = (uint8_t)(h >> 8);
+    }
+    if (q < 2) {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            o[2 + 8 * q + i] = (uint8_t)(((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4));
+    }
+    __syncthreads();
+    const int64_t nvalid = min((int64_t)Q40_BLOCKS_PER_WG, a.n_units - b0);
+    const int nbytes = (int)nvalid * 18;
+    uint8_t* dbase = a.dst + b0 * 18;
+    if ((reinterpret_cast<uintptr_t>(dbase) & 3) == 0) {
+        const int nw = nbytes >> 2;
+        const uint32_t* s4 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* d4 = reinterpret_cast<uint32_t*>(dbase);
+        for (int t = tid; t < nw; t += 256) d4[t] = s4[t];
+        for (int t = (nw << 2) + tid; t < nbytes; t += 256) dbase[t] = stage[t];
+    } else {
+        for (int t = tid; t < nbytes; t += 256) dbase[t] = stage[t];
+    }
+}
+
+// ------------------------------------------------------------------
+// shared LDS layout of the superblock kernels
+// ------------------------------------------------------------------
+template <int SPW, int BYTES>
+struct alignas(16) SbLds {
+    float v[SPW][QK_K];      // per-value staging for superblock sums
+    float tmp[SPW][40];
+    float sc[SPW][16], mn[SPW][16], sw[SPW][16];
+    float hdr[SPW][4];
+    int ls[SPW][16], lm[SPW][16];
+    uint8_t L[SPW][QK_K];
+    uint8_t out[SPW * BYTES + 16];
+};
+
+// finish: every valid superblock of the wave has its bytes in s.out
+template <int SPW, int BYTES>
+QS_DEV void sb_store(const SbLds<SPW, BYTES>& s, const KArgs& a) {
+    const int64_t first = (int64_t)blockIdx.x * SPW;
+    const int64_t nvalid = min((int64_t)SPW, a.n_units - first);
+    store_staged(s.out, a.dst, first * BYTES, (int)nvalid * BYTES);
+}
+
+// ------------------------------------------------------------------
+// Q4_K / Q5_K  (q4_k.py:25-79, q5_k.py:25-82)
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT, int NMAX>
+__global__ __launch_bounds__(64) void k_q45_k(KArgs a, Steps steps, QpSteps qps) {
+    constexpr int LPS = 8, SPW = 8, BYTES = NMAX == 15 ? 144 : 176;
+    constexpr float FMAX = (float)NMAX;
+    __shared__ SbLds<SPW, BYTES> s;
+    const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[32], w[32];
+    load_elems<SRC, true, 32>(a.src, p.elem, x);
+
+    if constexpr (IMAT) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) s.v[slot][32 * g + i] = x[i] * x[i];
+        wave_sync();
+        const float sum = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g);
+        const float sigma2 = (2.0f * sum) / 256.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float t = x[i] * x[i];
+            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
+        }
+    } else {
+        float t[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) t[i] = x[i] * x[i];
+        const float av = sqrtf(cascade8_sum(t) / 32.0f);
+#pragma unroll
+        for (int i = 0; i < 32; i++) w[i] = av + fabsf(x[i]);
+    }
+
+    const QkxResult r = qkx_fit<32, false>(x, w, steps, FMAX);
+    s.sc[slot][g] = r.scale;
+    s.mn[slot][g] = r.the_min;
+    if constexpr (IMAT) s.sw[slot][g] = cascade8_sum(w);
+    wave_sync();
+
+    int ls, lm;
+    float d16, m16;
+    if constexpr (IMAT) {
+        if (g < 2) {
+            float xv[8], wv[8], L[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                xv[i] = g == 0 ? s.sc[slot][i] : s.mn[slot][i];
+                wv[i] = s.sw[slot][i];
+            }
+            const float sc = qp_fit<8>(xv, wv, 63, qps.v, L);
+            s.hdr[slot][g] = sc;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int li = (int)L[i] & 0xFF;
+                if (g == 0) s.ls[slot][i] = li;
+                else s.lm[slot][i] = li;
+            }
+        }
+        wave_sync();
+        d16 = f16_round(s.hdr[slot][0]);
+        m16 = f16_round(s.hdr[slot][1]);
+        ls = s.ls[slot][g];
+        lm = s.lm[slot][g];
+    } else {
+        float ms = s.sc[slot][0], mm = s.mn[slot][0];
+#pragma unroll
+        for (int j = 1; j < 8; j++) {
+            ms = fmaxf(ms, s.sc[slot][j]);
+            mm = fmaxf(mm, s.mn[slot][j]);
+        }
+        const float inv_s = ms > 0 ? rdiv(63.0f, ms) : 0.0f;
+        const float inv_m = mm > 0 ? rdiv(63.0f, mm) : 0.0f;
+        const int la = (int)rintf(inv_s * r.scale) & 0xFF, lb = (int)rintf(inv_m * r.the_min) & 0xFF;
+        ls = la > 63 ? 63 : la;
+        lm = lb > 63 ? 63 : lb;
+        d16 = f16_round(ms / 63.0f);
+        m16 = f16_round(mm / 63.0f);
+        wave_sync();
+        s.ls[slot][g] = ls;
+        s.lm[slot][g] = lm;
+    }
+
+    const float dg = d16 * (float)(ls & 63), mg = m16 * (float)(lm & 63);
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float v;
+        if (dg != 0.0f) {
+            const float t = x[i] + mg;
+            v = clampf(rintf(t / dg), 0.0f, FMAX);
+        } else {
+            v = qkx_level(r, x[i], FMAX);
+        }
+        s.L[slot][32 * g + i] = (uint8_t)(int)v;
+    }
+    if (g == 0) {
+        s.hdr[slot][2] = __builtin_bit_cast(float, f16_bits(d16));
+        s.hdr[slot][3] = __builtin_bit_cast(float, f16_bits(m16));
+    }
+    wave_sync();
+
+    // pack (q4_k.py:70-78, q5_k.py:70-81)
+    const uint8_t* L = s.L[slot];
+    const int* LS = s.ls[slot];
+    const int* LM = s.lm[slot];
+    uint8_t* o = s.out + slot * BYTES;
+    const uint32_t dbits = __builtin_bit_cast(uint32_t, s.hdr[slot][2]);
+    const uint32_t mbits = __builtin_bit_cast(uint32_t, s.hdr[slot][3]);
+    for (int bi = g; bi < BYTES; bi += LPS) {
+        uint32_t v;
+        if (bi < 2) v = dbits >> (8 * bi);
+        else if (bi < 4) v = mbits >> (8 * (bi - 2));
+        else if (bi < 8) { const int j = bi - 4; v = LS[j] | ((LS[4 + j] >> 4) << 6); }
+        else if (bi < 12) { const int j = bi - 8; v = LM[j] | ((LM[4 + j] >> 4) << 6); }
+        else if (bi < 16) { const int j = bi - 12; v = (LS[4 + j] & 15) | ((LM[4 + j] & 15) << 4); }
+        else if (NMAX == 31 && bi < 48) {
+            const int l = bi - 16;
+            v = 0;
+#pragma unroll
+            for (int sb = 0; sb < 8; sb++) v |= ((L[32 * sb + l] >> 4) & 1u) << sb;
+        } else {
+            const int t = bi - (NMAX == 31 ? 48 : 16), j = t >> 5, l = t & 31;
+            v = (L[64 * j + l] & 15u) | ((L[64 * j + 32 + l] & 15u) << 4);
+        }
+        o[bi] = (uint8_t)v;
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// Q6_K  (q6_k.py:22-65)
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT>
+__global__ __launch_bounds__(64) void k_q6_k(KArgs a, Steps steps) {
+    constexpr int LPS = 16, SPW = 4, BYTES = 210;
+    __shared__ SbLds<SPW, BYTES> s;
+    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[16], w[16];
+    load_elems<SRC, true, 16>(a.src, p.elem, x);
+#pragma unroll
+    for (int i = 0; i < 16; i++) w[i] = IMAT ? a.qw[p.col + i] : x[i] * x[i];
+
+    const QxResult r = qx_fit<16>(x, w, 32, steps);
+    s.sc[slot][g] = r.scale;
+    wave_sync();
+    float sc16[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) sc16[j] = s.sc[slot][j];
+    float amax;
+    const float max_scale = absmax_first(sc16, amax);
+    const bool live = amax >= GROUP_MAX_EPS;
+    const float iscale = rdiv(-128.0f, live ? max_scale : 1.0f);
+    const float d16 = f16_round(live ? 1.0f / iscale : 0.0f);
+    int sc8 = (int)fminf(rintf(iscale * r.scale), 127.0f);
+    sc8 = ((sc8 & 0xFF) ^ 0x80) - 0x80;
+    const float dq = d16 * (float)sc8;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float v;
+        if (dq != 0.0f) v = clampf(rintf(x[i] / dq), -32.0f, 31.0f) + 32.0f;
+        else v = qx_level(r, x[i], 32.0f);
+        s.L[slot][16 * g + i] = live ? (uint8_t)(int)v : (uint8_t)0;
+    }
+    s.ls[slot][g] = live ? sc8 : 0;
+    if (g == 0) s.hdr[slot][0] = __builtin_bit_cast(float, f16_bits(d16));
+    wave_sync();
+
+    // pack (q6_k.py:55-64)
+    const uint8_t* L = s.L[slot];
+    uint8_t* o = s.out + slot * BYTES;
+    const uint32_t dbits = __builtin_bit_cast(uint32_t, s.hdr[slot][0]);
+    for (int bi = g; bi < BYTES; bi += LPS) {
+        uint32_t v;
+        if (bi < 128) {
+            const int h = bi >> 6, rr = bi & 63;
+            const uint8_t* q = L + 128 * h + (rr & 31) + (rr >= 32 ? 32 : 0);
+            v = (q[0] & 15u) | ((q[64] & 15u) << 4);
+        } else if (bi < 192) {
+            const int t = bi - 128, h = t >> 5, l = t & 31;
+            const uint8_t* q = L + 128 * h + l;
+            v = (q[0] >> 4) | ((q[32] >> 4) << 2) | ((q[64] >> 4) << 4) | ((q[96] >> 4) << 6);
+        } else if (bi < 208) {
+            v = (uint32_t)s.ls[slot][bi - 192] & 0xFFu;
+        } else {
+            v = dbits >> (8 * (bi - 208));
+        }
+        o[bi] = (uint8_t)v;
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// Q3_K  (q3_k.py:23-78)
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT>
+__global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps32) {
+    constexpr int LPS = 16, SPW = 4, BYTES = 110;
+    __shared__ SbLds<SPW, BYTES> s;
+    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[16];
+    load_elems<SRC, true, 16>(a.src, p.elem, x);
+
+    float Lg[16];
+    int ls6;
+    float d16;
+    if constexpr (!IMAT) {
+        const float scale = q3_fit<16>(x, 4, Lg);
+        s.sc[slot][g] = scale;
+        wave_sync();
+        float sc16[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) sc16[j] = s.sc[slot][j];
+        float amax;
+        const float max_scale = absmax_first(sc16, amax);
+        const bool has = max_scale != 0.0f;
+        const float iscale = rdiv(-32.0f, has ? max_scale : 1.0f);
+        int l = (int)rintf(iscale * scale);
+        l = ((l & 0xFF) ^ 0x80) - 0x80;
+        l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        ls6 = has ? l + 32 : 0;
+        d16 = f16_round(has ? 1.0f / iscale : 0.0f);
+    } else {
+        float w[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
+        wave_sync();
+        const float sigma2 = (2.0f * sb_seq_256(s.v[slot])) / 256.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float t = x[i] * x[i];
+            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
+        }
+        const QxResult r = qx_fit<16>(x, w, 4, steps4);
+#pragma unroll
+        for (int i = 0; i < 16; i++) Lg[i] = qx_level(r, x[i], 4.0f);
+        s.sc[slot][g] = r.scale;
+        s.sw[slot][g] = seq_sum(w);
+        wave_sync();
+        if (g == 0) {
+            float sc16[16], sw16[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                sc16[j] = s.sc[slot][j];
+                sw16[j] = s.sw[slot][j];
+            }
+            const QxResult r2 = qx_fit<16>(sc16, sw16, 32, steps32);
+            s.hdr[slot][0] = r2.scale;
+#pragma unroll
+            for (int j = 0; j < 16; j++) s.ls[slot][j] = (int)qx_level(r2, sc16[j], 32.0f);
+        }
+        wave_sync();
+        ls6 = s.ls[slot][g];
+        d16 = f16_round(s.hdr[slot][0]);
+    }
+
+    const float dq = d16 * (float)(ls6 - 32);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float v = dq != 0.0f ? clampf(rintf(x[i] / dq), -4.0f, 3.0f) + 4.0f : Lg[i];
+        s.L[slot][16 * g + i] = (uint8_t)(int)v;
+    }
+    wave_sync();
+    s.ls[slot][g] = ls6;
+    if (g == 0) s.hdr[slot][1] = __builtin_bit_cast(float, f16_bits(d16));
+    wave_sync();
+
+    // pack (q3_k.py:61-77)
+    const uint8_t* L = s.L[slot];
+    const int* LS = s.ls[slot];
+    uint8_t* o = s.out + slot * BYTES;
+    const uint32_t dbits = __builtin_bit_cast(uint32_t, s.hdr[slot][1]);
+    for (int bi = g; bi < BYTES; bi += LPS) {
+        uint32_t v = 0;
+        if (bi < 32) {
+#pragma unroll
+            for (int b = 0; b < 8; b++) v |= (L[32 * b + bi] > 3 ? 1u : 0u) << b;
+        } else if (bi < 96) {
+            const int t = bi - 32, h = t >> 5, l = t & 31;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint32_t q = L[128 * h + 32 * i + l];
+                q = q > 3 ? q - 4 : q;
+                v |= q << (2 * i);
+            }
+        } else if (bi < 104) {
+            const int j = bi - 96;
+            v = (LS[j] & 15) | ((LS[j + 8] & 15) << 4);
+        } else if (bi < 108) {
+            const int i = bi - 104;
+            v = (LS[i] >> 4) | ((LS[4 + i] >> 4) << 2) | ((LS[8 + i] >> 4) << 4) | ((LS[12 + i] >> 4) << 6);
+        } else {
+            v = dbits >> (8 * (bi - 108));
+        }
+        o[bi] = (uint8_t)v;
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// Q2_K  (q2_k.py:25-81)
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT>
+__global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) {
+    constexpr int LPS = 16, SPW = 4, BYTES = 84;
+    __shared__ SbLds<SPW, BYTES> s;
+    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[16], w[16];
+    load_elems<SRC, true, 16>(a.src, p.elem, x);
+
+    QkxResult r;
+    int ls, lm;
+    float d16, m16;
+    if constexpr (!IMAT) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) w[i] = fabsf(x[i]);
+        r = qkx_fit<16, true>(x, w, steps, 3.0f);
+        s.sc[slot][g] = r.scale;
+        s.mn[slot][g] = r.the_min;
+        wave_sync();
+        float ms = s.sc[slot][0], mm = s.mn[slot][0];
+#pragma unroll
+        for (int j = 1; j < 16; j++) {
+            ms = fmaxf(ms, s.sc[slot][j]);
+            mm = fmaxf(mm, s.mn[slot][j]);
+        }
+        const bool pos_s = ms > 0, pos_m = mm > 0;
+        const float inv_s = pos_s ? 15.0f / ms : 0.0f;
+        const float inv_m = pos_m ? 15.0f / mm : 0.0f;
+        ls = (int)rintf(inv_s * r.scale) & 0xFF;
+        lm = (int)rintf(inv_m * r.the_min) & 0xFF;
+        d16 = f16_round(pos_s ? ms / 15.0f : 0.0f);
+        m16 = f16_round(pos_m ? mm / 15.0f : 0.0f);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
+        wave_sync();
+        const float sigma2 = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g) / 256.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float t = x[i] * x[i];
+            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
+        }
+        r = qkx_fit<16, false>(x, w, steps, 3.0f);
+        s.sc[slot][g] = r.scale;
+        s.mn[slot][g] = r.the_min;
+        s.sw[slot][g] = cascade8_sum(w);
+        wave_sync();
+        if (g < 2) {
+            float xv[16], wv[16], L[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                xv[i] = g == 0 ? s.sc[slot][i] : s.mn[slot][i];
+                wv[i] = s.sw[slot][i];
+            }
+            const float sc = qp_fit<16>(xv, wv, 15, qps.v, L);
+            s.hdr[slot][g] = sc;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int li = (int)L[i] & 0xFF;
+                if (g == 0) s.ls[slot][i] = li;
+                else s.lm[slot][i] = li;
+            }
+        }
+        wave_sync();
+        d16 = f16_round(s.hdr[slot][0]);
+        m16 = f16_round(s.hdr[slot][1]);
+        ls = s.ls[slot][g];
+        lm = s.lm[slot][g];
+    }
+    const int scb = (ls | (lm << 4)) & 0xFF;
+    const float dg = d16 * (float)(scb & 15), mg = m16 * (float)(scb >> 4);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        float v;
+        if (dg != 0.0f) {
+            const float t = x[i] + mg;
+            v = clampf(rintf(t / dg), 0.0f, 3.0f);
+        } else {
+            v = qkx_level(r, x[i], 3.0f);
+        }
+        s.L[slot][16 * g + i] = (uint8_t)(int)v;
+    }
+    wave_sync();
+    s.ls[slot][g] = scb;
+    if (g == 0) {
+        s.hdr[slot][2] = __builtin_bit_cast(float, f16_bits(d16));
+        s.hdr[slot][3] = __builtin_bit_cast(float, f16_bits(m16));
+    }
+    wave_sync();
+
+    // pack (q2_k.py:74-80)
+    const uint8_t* L = s.L[slot];
+    uint8_t* o = s.out + slot * BYTES;
+    const uint32_t dbits = __builtin_bit_cast(uint32_t, s.hdr[slot][2]);
+    const uint32_t mbits = __builtin_bit_cast(uint32_t, s.hdr[slot][3]);
+    for (int bi = g; bi < BYTES; bi += LPS) {
+        uint32_t v = 0;
+        if (bi < 16) v = (uint32_t)s.ls[slot][bi];
+        else if (bi < 80) {
+            const int t = bi - 16, h = t >> 5, l = t & 31;
+#pragma unroll
+            for (int i = 0; i < 4; i++) v |= (uint32_t)L[128 * h + 32 * i + l] << (2 * i);
+        } else if (bi < 82) v = dbits >> (8 * (bi - 80));
+        else v = mbits >> (8 * (bi - 82));
+        o[bi] = (uint8_t)v;
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// IQ4_XS  (iq4_xs.py:149-188)
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT>
+__global__ __launch_bounds__(64) void k_iq4_xs(KArgs a) {
+    constexpr int LPS = 8, SPW = 8, BYTES = 136;
+    __shared__ SbLds<SPW, BYTES> s;
+    const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[32], w[32];
+    load_elems<SRC, true, 32>(a.src, p.elem, x);
+    if constexpr (IMAT) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) s.v[slot][32 * g + i] = x[i] * x[i];
+        wave_sync();
+        const float sigma2 = (2.0f * sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g)) / 256.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const float t = x[i] * x[i];
+            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
+    }
+    const float scale = iq4_scale_search(x, w);
+    s.sc[slot][g] = scale;
+    wave_sync();
+    float sc8[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) sc8[j] = s.sc[slot][j];
+    float amax;
+    const float max_scale = absmax_first(sc8, amax);
+    const float d = -max_scale / 32.0f;
+    const float idq = d != 0.0f ? 1.0f / d : 0.0f;
+    const float lsf = clampf(rintf(idq * scale), -32.0f, 31.0f);
+    const float dl = d * lsf;
+    const float idl = dl != 0.0f ? 1.0f / dl : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) s.L[slot][32 * g + i] = (uint8_t)iq4_index(idl * x[i]);
+    s.ls[slot][g] = (int)(lsf + 32.0f);
+    if (g == 0) s.hdr[slot][0] = __builtin_bit_cast(float, f16_bits(d));
+    wave_sync();
+
+    const uint8_t* L = s.L[slot];
+    const int* LS = s.ls[slot];
+    uint8_t* o = s.out + slot * BYTES;
+    const uint32_t dbits = __builtin_bit_cast(uint32_t, s.hdr[slot][0]);
+    for (int bi = g; bi < BYTES; bi += LPS) {
+        uint32_t v;
+        if (bi < 2) v = dbits >> (8 * bi);
+        else if (bi < 4) {
+            uint32_t hb = 0;
+#pragma unroll
+            for (int b = 0; b < 8; b++) hb |= (uint32_t)(LS[b] >> 4) << (2 * b);
+            v = hb >> (8 * (bi - 2));
+        } else if (bi < 8) {
+            const int j = bi - 4;
+            v = (LS[2 * j] & 15) | ((LS[2 * j + 1] & 15) << 4);
+        } else {
+            const int t = bi - 8, blk = t >> 4, j = t & 15;
+            v = L[32 * blk + j] | (L[32 * blk + 16 + j] << 4);
+        }
+        o[bi] = (uint8_t)v;
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+}  // namespace qs

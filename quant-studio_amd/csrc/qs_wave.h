@@ -1,0 +1,106 @@
+// Wave-level plumbing shared by the superblock kernels: one 64-lane workgroup
+// quantizes SB_PER_WAVE superblocks, LPS lanes per superblock. Cross-lane
+// reductions of a superblock go through LDS in the exact order the reference's
+// sums use; the packed output is staged in LDS and written with coalesced
+// dword stores.
+#pragma once
+
+#include "qs_device.h"
+
+namespace qs {
+
+// Wave-synchronous barrier for a one-wave workgroup: orders LDS traffic
+// between lanes.
+QS_DEV void wave_sync() { __syncthreads(); }
+
+// Superblock position of this lane.
+struct SbPos {
+    int64_t sb;      // global superblock index (clamped copy used for loads)
+    bool valid;      // sb < n_sb
+    int slot;        // superblock slot within the wave
+    int g;           // group index within the superblock (lane's group)
+    int64_t elem;    // element offset of the lane's group in the source
+    int64_t col;     // column of the lane's group start within its row
+};
+
+template <int LPS, int GROUP>
+QS_DEV SbPos sb_pos(int64_t n_sb, int64_t sb_per_row, int64_t stride) {
+    constexpr int SPW = 64 / LPS;
+    SbPos p;
+    const int lane = threadIdx.x;
+    p.slot = lane / LPS;
+    p.g = lane % LPS;
+    const int64_t sb = (int64_t)blockIdx.x * SPW + p.slot;
+    p.valid = sb < n_sb;
+    p.sb = p.valid ? sb : n_sb - 1;
+    const int64_t row = p.sb / sb_per_row;
+    p.col = (p.sb % sb_per_row) * QK_K + (int64_t)p.g * GROUP;
+    p.elem = row * stride + p.col;
+    return p;
+}
+
+// torch CPU `.sum(-1)` over one superblock's 256 values (8-lane cascade):
+// acc[a][l] = sum over i=0..7 (in order) of v[32i + 8a + l], p[l] =
+// ((acc0+acc1)+acc2)+acc3, result = +0 + p[0] + ... + p[7].
+// `v` is the superblock's 256 values in LDS; `tmp` holds 40 floats.
+template <int LPS>
+QS_DEV float sb_cascade8_256(const float* v, float* tmp, int g) {
+    constexpr int PER = 32 / LPS;
+#pragma unroll
+    for (int t = 0; t < PER; t++) {
+        const int j = g * PER + t;             // j = 8a + l
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = acc + v[32 * i + j];
+        tmp[j] = acc;
+    }
+    wave_sync();
+    if (g < 8) {
+        float p = tmp[g] + tmp[8 + g];
+        p = p + tmp[16 + g];
+        p = p + tmp[24 + g];
+        tmp[32 + g] = p;
+    }
+    wave_sync();
+    float fin = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) fin = fin + tmp[32 + l];
+    return fin;
+}
+
+// strict left-to-right sum of a superblock's 256 values held in LDS
+QS_DEV float sb_seq_256(const float* v) {
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    float s = v[0];
+    float4 q = v4[0];
+    s = s + q.y;
+    s = s + q.z;
+    s = s + q.w;
+#pragma unroll 8
+    for (int j = 1; j < 64; j++) {
+        q = v4[j];
+        s = s + q.x;
+        s = s + q.y;
+        s = s + q.z;
+        s = s + q.w;
+    }
+    return s;
+}
+
+// Copy the wave's staged output (nbytes at `stage`) to dst + off with
+// coalesced dword stores when the destination is 4-byte aligned.
+QS_DEV void store_staged(const uint8_t* stage, uint8_t* dst, int64_t off, int nbytes) {
+    const int lane = threadIdx.x;
+    uint8_t* d = dst + off;
+    if ((reinterpret_cast<uintptr_t>(d) & 3) == 0) {
+        const int nw = nbytes >> 2;
+        const uint32_t* s4 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* d4 = reinterpret_cast<uint32_t*>(d);
+        for (int t = lane; t < nw; t += 64) d4[t] = s4[t];
+        for (int t = (nw << 2) + lane; t < nbytes; t += 64) d[t] = stage[t];
+    } else {
+        for (int t = lane; t < nbytes; t += 64) d[t] = stage[t];
+    }
+}
+
+}  // namespace qs

@@ -127,6 +127,13 @@ def make_cases() -> dict[str, dict[str, np.ndarray]]:
     rows, k = 8, 512
     a = (rng.standard_normal((rows, k)) * 0.05).astype(np.float32)
     cases["f32"] = dict(x=a, imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
+
+    # superblocks on which plausible restatement slips change the output
+    # (chosen by select_sensitive.py; inputs only)
+    sens = HERE / "sensitive.npz"
+    if sens.exists():
+        z = np.load(sens)
+        cases["sensitive"] = dict(x=z["x"], imat=z["imat"])
     return cases
 
 

@@ -1,0 +1,95 @@
+"""CPU tests of the C-ABI library: it loads, exports every function the public
+header declares, reports the reference's type table, and rejects bad
+arguments before any device work (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from golden_data import TYPES
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "quant_studio.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(qs_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_api():
+    names = set(declared_functions())
+    assert {"qs_abi_version", "qs_row_bytes", "qs_quantize", "qs_last_error",
+            "qs_type_supported", "qs_type_needs_imatrix", "qs_type_uses_imatrix"} <= names
+
+
+def test_library_exports_every_declared_symbol(qs):
+    L = qs.library()
+    for name in declared_functions():
+        assert hasattr(L, name), f"libqs_hip.so does not export {name}"
+    assert L.qs_abi_version() == 1
+
+
+@pytest.mark.parametrize("qtype", sorted(TYPES))
+def test_row_bytes_match_reference_block_sizes(qs, qtype):
+    tid, blk, nbytes = TYPES[qtype]
+    L = qs.library()
+    assert L.qs_row_bytes(tid, 4 * blk) == 4 * nbytes
+    assert L.qs_row_bytes(tid, blk + 1) == -22
+    assert L.qs_row_bytes(tid, 0) == -22
+
+
+def test_type_flags_match_reference_specs(qs):
+    L = qs.library()
+    for name, spec in qs.ALL_SPECS.items():
+        t = int(spec.ggml_type)
+        assert L.qs_type_needs_imatrix(t) == int(spec.needs_imatrix), name
+        assert L.qs_type_uses_imatrix(t) == int(spec.uses_imatrix), name
+    assert L.qs_type_needs_imatrix(99) == -95
+
+
+def test_registry_lists_only_types_with_kernels(qs):
+    L = qs.library()
+    for name, spec in qs.ALL_SPECS.items():
+        assert (name in qs.QUANT_TYPES) == bool(L.qs_type_supported(int(spec.ggml_type)))
+    for name in ("q4_0", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_xs"):
+        assert name in qs.QUANT_TYPES
+
+
+def _call(L, t, src_type=30, src=16, n=4, k=256, stride=512, qw=None, dst=64, dst_bytes=10 ** 6):
+    return L.qs_quantize(t, src_type, ctypes.c_void_p(src), n, k, stride,
+                         None if qw is None else ctypes.c_void_p(qw), ctypes.c_void_p(dst),
+                         dst_bytes, None)
+
+
+def test_quantize_rejects_bad_arguments_before_launch(qs):
+    L = qs.library()
+    assert _call(L, 99) == -95                       # unknown type
+    assert _call(L, 12, k=100) == -22                # k not a multiple of 256
+    assert _call(L, 12, src_type=5) == -22           # unsupported source dtype
+    assert _call(L, 12, n=-1) == -22
+    assert _call(L, 12, src=0) == -22                # null source
+    assert _call(L, 12, src=8) == -22                # misaligned source
+    assert _call(L, 12, stride=500) == -22           # stride below k*2 / not 16-aligned
+    assert _call(L, 12, dst_bytes=10) == -22         # dst too small
+    assert b"dst holds 10 bytes" in L.qs_last_error()
+    assert _call(L, 12, n=0) == 0                    # empty input: no work, no launch
+
+
+def test_needs_imatrix_types_reject_missing_imatrix(qs):
+    L = qs.library()
+    for name, spec in qs.ALL_SPECS.items():
+        if spec.needs_imatrix and L.qs_type_supported(int(spec.ggml_type)):
+            assert _call(L, int(spec.ggml_type)) == -22
+            assert b"requires an imatrix" in L.qs_last_error()
+
+
+def test_quant_fn_refuses_cpu_tensors(qs):
+    import torch
+    fn = qs.QUANT_TYPES["q4_k"].make_kernel(torch.device("cpu"), None)
+    with pytest.raises(ValueError, match="ROCm device"):
+        fn(torch.zeros(2, 256))

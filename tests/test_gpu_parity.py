@@ -1,0 +1,149 @@
+"""GPU parity: the HIP quantizers against the reference's golden vectors and the
+CPU oracle, byte for byte. Runs on an MI355X (pytest -m gpu); every call goes
+through the C ABI of libqs_hip.so."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from golden_data import ORACLE_TYPES, TYPES, block_identical, cases
+
+pytestmark = pytest.mark.gpu
+
+HIP_TYPES = ORACLE_TYPES  # types with a HIP kernel and an oracle restatement
+NTHREADS = min(16, len(os.sched_getaffinity(0)))
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return torch.device("cuda:0")
+
+
+def to_device(x: np.ndarray, dev) -> torch.Tensor:
+    if x.dtype == np.uint16:
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(dev)
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev)
+
+
+def hip_quantize(qs, qtype, x, qw, dev) -> np.ndarray:
+    tid = TYPES[qtype][0]
+    xq = to_device(x, dev)
+    q = None if qw is None else torch.from_numpy(qw).to(dev)
+    out = qs.quantize(tid, xq, q)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("qtype", HIP_TYPES)
+def test_golden_vectors(qs, dev, qtype):
+    for key, x, qw, expect in cases(qtype):
+        print(f"{qtype} {key} shape={x.shape}", flush=True)
+        got = hip_quantize(qs, qtype, x, qw, dev)
+        same = block_identical(got, expect, qtype)
+        assert same.all(), f"{qtype} {key}: {int((~same).sum())}/{same.size} blocks differ"
+
+
+def c2_like(rows: int, k: int, seed: int):
+    rng = np.random.default_rng(seed)
+    a = rng.standard_normal((rows, k)) * 0.02 * np.exp(0.3 * rng.standard_normal((rows, 1)))
+    return bf16_bits(a), rng.lognormal(0.0, 1.0, k).astype(np.float32)
+
+
+@pytest.mark.parametrize("qtype", HIP_TYPES)
+@pytest.mark.parametrize("imat", [False, True])
+def test_oracle_parity_random(qs, dev, qtype, imat):
+    if qtype == "q4_0" and imat:
+        pytest.skip("Q4_0 ignores an imatrix")
+    x, qw = c2_like(384, 2560, seed=sum(map(ord, qtype)) * 2 + int(imat))
+    qw = qw if imat else None
+    print(f"{qtype} imat={imat} 384x2560", flush=True)
+    got = hip_quantize(qs, qtype, x, qw, dev)
+    ref = oracle.quantize(qtype, x, qw, n_threads=NTHREADS)
+    same = block_identical(got, ref, qtype)
+    assert same.all(), f"{int((~same).sum())}/{same.size} blocks differ"
+
+
+def test_q4_0_full_4096x4096(qs, dev):
+    """BASELINE config: Q4_0 on one bf16 4096x4096 tensor, N(0, 0.02) with 0.1%
+    outliers x20, seed 0, byte-exact."""
+    rng = np.random.default_rng(0)
+    a = rng.normal(0.0, 0.02, (4096, 4096))
+    idx = rng.choice(a.size, 16777, replace=False)
+    a.reshape(-1)[idx] *= 20.0
+    x = bf16_bits(a)
+    got = hip_quantize(qs, "q4_0", x, None, dev)
+    ref = oracle.quantize("q4_0", x, None, n_threads=NTHREADS)
+    assert got.shape == (4096, 4096 // 32 * 18)
+    assert np.array_equal(got, ref)
+
+
+def test_q4_k_imatrix_full_ffn_shapes(qs, dev):
+    """BASELINE config: Q4_K with imatrix on 9728x2560 and 2560x9728 bf16,
+    per-row log-normal std jitter, log-normal per-column imatrix."""
+    for rows, k, seed in ((9728, 2560, 1), (2560, 9728, 2)):
+        print(f"q4_k imat {rows}x{k}", flush=True)
+        x, qw = c2_like(rows, k, seed)
+        got = hip_quantize(qs, "q4_k", x, qw, dev)
+        ref = oracle.quantize("q4_k", x, qw, n_threads=NTHREADS)
+        same = block_identical(got, ref, "q4_k")
+        assert same.all(), f"{rows}x{k}: {int((~same).sum())}/{same.size} blocks differ"
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q4_k", "q6_k", "q3_k"])
+def test_row_chunking_invariance(qs, dev, qtype):
+    x, qw = c2_like(300, 1024, seed=9)
+    tid = TYPES[qtype][0]
+    xd = to_device(x, dev)
+    q = torch.from_numpy(qw).to(dev)
+    whole = qs.quantize(tid, xd, q)
+    parts = torch.cat([qs.quantize(tid, xd[a:b], q) for a, b in ((0, 7), (7, 150), (150, 300))])
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q5_k", "q2_k", "iq4_xs"])
+def test_f16_source(qs, dev, qtype):
+    rng = np.random.default_rng(4)
+    a = (rng.standard_normal((64, 512)) * 0.05).astype(np.float16)
+    qw = rng.lognormal(0, 1, 512).astype(np.float32)
+    tid = TYPES[qtype][0]
+    got = qs.quantize(tid, torch.from_numpy(a).to(dev), torch.from_numpy(qw).to(dev)).cpu().numpy()
+    ref = oracle.quantize(qtype, a.astype(np.float32), None if qtype == "q4_0" else qw)
+    assert np.array_equal(got, ref)
+
+
+def test_row_stride_and_unaligned_output(qs, dev):
+    x, qw = c2_like(40, 1024, seed=12)
+    wide = torch.zeros((40, 1024 + 64), dtype=torch.bfloat16, device=dev)
+    wide[:, :1024] = to_device(x, dev)
+    view = wide[:, :1024]                       # row stride 1088 elements (2176 B)
+    assert view.stride(0) == 1088
+    for qtype in ("q4_0", "q6_k", "q4_k"):
+        tid = TYPES[qtype][0]
+        rb = TYPES[qtype][2] * (1024 // TYPES[qtype][1])
+        buf = torch.zeros(40 * rb + 3, dtype=torch.uint8, device=dev)
+        out = buf[1:1 + 40 * rb]                # 1-byte offset: byte-store path
+        qs.quantize(tid, view, torch.from_numpy(qw).to(dev), out=out)
+        ref = oracle.quantize(qtype, x, None if qtype == "q4_0" else qw)
+        b = buf.cpu().numpy()
+        assert b[0] == 0 and b[-2:].tolist() == [0, 0]
+        assert np.array_equal(b[1:1 + 40 * rb].reshape(40, rb), ref)
+
+
+def test_empty_and_single_row(qs, dev):
+    e = torch.zeros((0, 256), dtype=torch.bfloat16, device=dev)
+    assert qs.quantize(12, e, None).shape == (0, 144)
+    x, qw = c2_like(1, 256, seed=3)
+    got = hip_quantize(qs, "q4_k", x, qw, dev)
+    assert np.array_equal(got, oracle.quantize("q4_k", x, qw))

@@ -1,0 +1,127 @@
+"""CPU tests that pin the oracle before anything is checked against it.
+
+- every supported type against the golden vectors the reference itself wrote
+  (tests/golden/gen_golden.py imports the reference's kernels/*.py and runs
+  its eager CPU quantizers);
+- the reduction orders against torch's own CPU reductions (the runtime the
+  reference's eager path runs on), the fp16 conversion against numpy;
+- closed-form known answers for Q4_0, and planted mistakes in the oracle
+  (wrong division form, sum order, rounding, accept test, a dropped
+  candidate) that the golden vectors must each expose.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from golden_data import ORACLE_TYPES, block_identical, cases
+
+
+@pytest.mark.parametrize("qtype", ORACLE_TYPES)
+def test_oracle_matches_reference_golden(qtype):
+    for key, x, qw, expect in cases(qtype):
+        got = oracle.quantize(qtype, x, qw, n_threads=4)
+        same = block_identical(got, expect, qtype)
+        assert same.all(), f"{qtype} {key}: {int((~same).sum())} of {same.size} blocks differ"
+
+
+@pytest.mark.parametrize("n", [8, 16, 32, 256])
+def test_cascade8_is_torch_row_sum(n):
+    rng = np.random.default_rng(n)
+    rows = rng.standard_normal((2000, n)).astype(np.float32)
+    rows[::7] *= rng.lognormal(0, 3, (rows[::7].shape[0], 1)).astype(np.float32)
+    rows[::11] = np.abs(rows[::11]) ** 3
+    ref = torch.from_numpy(rows).sum(-1).numpy()
+    got = np.array([oracle.sum_cascade8(r) for r in rows], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("n", [16, 32])
+def test_tree_sum_is_adjacent_pairs(n):
+    rng = np.random.default_rng(5)
+    for _ in range(500):
+        v = rng.standard_normal(n).astype(np.float32) * np.float32(rng.lognormal(0, 2))
+        t = v.copy()
+        while t.size > 1:
+            t = (t[0::2] + t[1::2]).astype(np.float32)
+        assert oracle.sum_tree(v) == t[0]
+
+
+def test_f16_round_to_nearest_even():
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * np.float32(1e-3),
+        rng.standard_normal(4000).astype(np.float32) * np.float32(1e-6),   # f16 subnormal range
+        rng.standard_normal(2000).astype(np.float32) * np.float32(3e4),
+        # exact ties between two f16 neighbours (normal and subnormal)
+        (np.arange(1, 1000, dtype=np.float32) * np.float32(2.0 ** -11) + np.float32(2.0 ** -12)),
+        (np.arange(1, 1000, dtype=np.float32) * np.float32(2.0 ** -24) + np.float32(2.0 ** -25)),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e-8, -2.0 ** -25, 2.0 ** -24], np.float32),
+    ])
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_f16_bits(v) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_python_float_over_tensor_is_reciprocal_multiply():
+    """torch evaluates `c / t` (c a Python float) as t.reciprocal() * c, which the
+    oracle's RDIV restates; on these inputs it differs from IEEE c / t."""
+    rng = np.random.default_rng(11)
+    t = (rng.standard_normal(20000) * 3).astype(np.float32)
+    for c in (63.0, -32.0, -128.0, 4.0, 15.0, -4.1, 31.9):
+        got = (c / torch.from_numpy(t)).numpy()
+        recip = (np.float32(1.0) / t).astype(np.float32) * np.float32(c)
+        ieee = (np.float32(c) / t).astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), recip.view(np.uint32))
+        if np.log2(abs(c)) % 1:   # a power-of-two c scales exactly: both forms agree
+            assert not np.array_equal(got.view(np.uint32), ieee.view(np.uint32))
+
+
+def test_q4_0_known_answer():
+    # block [-8..7]*s: max |x| is -8s (first), d = -8s/-8 = s, levels x/s + 8
+    s = np.float32(0.125)
+    x = (np.arange(-8, 8, dtype=np.float32) * s)
+    x = np.concatenate([x, x])[None, :]
+    out = oracle.quantize("q4_0", x)[0]
+    assert out[:2].view(np.float16)[0] == np.float16(s)
+    q = np.concatenate([np.arange(16), np.arange(16)])
+    assert np.array_equal(out[2:], (q[:16] | (q[16:] << 4)).astype(np.uint8))
+
+
+def test_q4_0_all_zero_block():
+    out = oracle.quantize("q4_0", np.zeros((1, 32), np.float32))[0]
+    # d = 0 / -8.0 = -0.0 (fp16 0x8000), id = 0, every level floor(0*0 + 8.5) = 8
+    assert out[:2].tolist() == [0x00, 0x80] and (out[2:] == 0x88).all()
+
+
+# planted mistakes in the oracle (qso_set_mutation) and a type whose golden
+# vectors must expose each one
+MUTANTS = {
+    1: ("rdiv as IEEE division", ["q3_k", "q6_k", "iq4_xs"]),
+    2: ("sequential sum for torch .sum(-1)", ["q4_k", "q2_k", "iq4_xs"]),
+    3: ("sequential sum for tree_sum", ["q4_k", "q5_k", "q2_k"]),
+    4: ("last make_qkx candidate dropped", ["q4_k", "q5_k", "q2_k"]),
+    5: ("round half away from zero", ["q4_k", "q3_k", "q6_k"]),
+    6: ("make_qx accept with >=", ["q6_k", "q3_k"]),
+}
+
+
+@pytest.mark.parametrize("mut", sorted(MUTANTS))
+def test_golden_vectors_catch_planted_mistake(mut):
+    what, types = MUTANTS[mut]
+    L = oracle.lib()
+    L.qso_set_mutation(mut)
+    try:
+        for qtype in types:
+            caught = False
+            for key, x, qw, expect in cases(qtype):
+                got = oracle.quantize(qtype, x, qw, n_threads=4)
+                if not block_identical(got, expect, qtype).all():
+                    caught = True
+                    break
+            assert caught, f"planted mistake '{what}' not detected by {qtype} golden vectors"
+    finally:
+        L.qso_set_mutation(0)
