@@ -124,6 +124,25 @@ def cpu_baseline(oracle, host, qws):
                       f"{SHAPES[1][0]}x{SHAPES[1][1]} ({n} values), {dt:.2f} s, one pass"}
 
 
+def copy_peak(torch, dev, steps: int, warmup: int) -> int:
+    """1 GiB device-to-device copy: measured HBM copy rate (read + write bytes)."""
+    nbytes = 1 << 30
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
+                      "ms_per_copy": round(dt * 1e3, 4),
+                      "copy_GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,6 +150,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--types", default="all", help="per-type table: all, none or a comma list")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="time a plain 1 GiB device copy instead (HBM copy peak, and the "
+                         "reference size for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counts)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this quantizer runs on one GPU; --gpus must be 1 "
@@ -142,6 +164,8 @@ def main() -> int:
     import oracle
 
     dev = torch.device("cuda:0")
+    if args.copy_only:
+        return copy_peak(torch, dev, args.steps, args.warmup)
     xs, qws, host = make_inputs(torch, dev)
     per_step_bytes = sum(2 * r * k for r, k in SHAPES)
     nrot = max(1, -(-ROTATE_BYTES // per_step_bytes))
