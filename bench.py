@@ -53,6 +53,17 @@ def make_inputs(torch, dev, seed: int = 0):
     return xs, qws, host
 
 
+def profiled_traffic() -> int | None:
+    """HBM bytes per launch of the headline kernel, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs summarised in profiles/ (scaled by a copy of known size)."""
+    f = ROOT / "profiles" / "counters_q4_k_imat_9728x2560.md"
+    if f.exists():
+        for ln in f.read_text().splitlines():
+            if ln.startswith("traffic_bytes_per_launch:"):
+                return int(ln.split(":")[1])
+    return None
+
+
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
     return 2 * n_elems + n_elems * OUT_BYTES_PER_256[qtype] // 256 + 4 * k
 
@@ -219,7 +230,8 @@ def main() -> int:
                    "types": "q4_k", "imatrix": True, "n_values": n_elems,
                    "parallelism": "1 GPU (no exchange)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
+                     "traffic": profiled_traffic(),
                      "kernel": "k_q45_k<bf16, imatrix, 15>", "kernel_ms": round(kms[0], 4),
                      "algorithmic_bytes": alg},
         "per_type": per_type,
