@@ -51,6 +51,8 @@ def lib() -> ctypes.CDLL:
         L.qso_sum_tree.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.qso_f32_to_f16.restype = ctypes.c_uint16
         L.qso_f32_to_f16.argtypes = [ctypes.c_float]
+        L.qso_set_sqrt_hook.restype = None
+        L.qso_set_sqrt_hook.argtypes = [ctypes.c_void_p]
         L.qso_set_mutation.restype = None
         L.qso_set_mutation.argtypes = [ctypes.c_int]
         _lib = L
@@ -84,6 +86,27 @@ def quantize(qtype: str, x: np.ndarray, qw: np.ndarray | None = None,
     if rc != 0:
         raise RuntimeError(f"oracle: quantize {qtype} failed ({rc})")
     return out
+
+
+SQRT_FN = ctypes.CFUNCTYPE(ctypes.c_float, ctypes.c_float)
+_hook_ref = None
+
+
+def use_torch_sqrt(enable: bool) -> None:
+    """Make the oracle take its square roots from torch's CPU sqrt (the routine
+    the reference's eager path calls) instead of IEEE sqrtf. Single-threaded
+    use only (the callback takes the GIL)."""
+    global _hook_ref
+    if enable:
+        import torch
+
+        def f(v):
+            return torch.sqrt(torch.tensor(v, dtype=torch.float32)).item()
+        _hook_ref = SQRT_FN(f)
+        lib().qso_set_sqrt_hook(ctypes.cast(_hook_ref, ctypes.c_void_p))
+    else:
+        lib().qso_set_sqrt_hook(None)
+        _hook_ref = None
 
 
 def sum_cascade8(v: np.ndarray) -> np.float32:

@@ -17,6 +17,7 @@
 #include "qs_oracle.h"
 
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -38,6 +39,14 @@ static inline float RDIV(float c, float t) {
     return r * c;
 }
 static inline float RINT(float v) { return g_mut == MUT_ROUND_AWAY ? roundf(v) : rintf(v); }
+
+/* Square root: IEEE sqrtf by default. The reference's torch.sqrt on CPU is a
+ * library routine that is not correctly rounded (about 0.6% of results are one
+ * ulp low); a test can install that routine here to reproduce the reference's
+ * weights exactly. */
+static float (*g_sqrt_hook)(float) = 0;
+void qso_set_sqrt_hook(float (*fn)(float)) { g_sqrt_hook = fn; }
+static inline float SQRT(float v) { return g_sqrt_hook ? g_sqrt_hook(v) : sqrtf(v); }
 static inline float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
 /* ------------------------------------------------------------------ */
@@ -398,7 +407,7 @@ static void make_q3(const float *x, int n, int nmax, float *scale_out, float *Lo
 static void imat_weights(const float *x, const float *qw, float sigma2, float *w) {
     for (int i = 0; i < QK_K; i++) {
         float t = x[i] * x[i];
-        w[i] = qw[i] * sqrtf(sigma2 + t);
+        w[i] = qw[i] * SQRT(sigma2 + t);
     }
 }
 
@@ -564,7 +573,7 @@ static void q45_k_block(const float *x, const float *qw, uint8_t *out, int nmax)
     if (!qw) {
         int ns = nmax == 15 ? qkx_steps(-1.0f, 0.1f, 20, 15, steps) : qkx_steps(-0.5f, 0.1f, 15, 31, steps);
         for (int g = 0; g < 8; g++) {
-            float av_x = sqrtf(sumsq_c8(x + 32 * g, 32) / 32.0f);
+            float av_x = SQRT(sumsq_c8(x + 32 * g, 32) / 32.0f);
             for (int i = 0; i < 32; i++) w[32 * g + i] = av_x + fabsf(x[32 * g + i]);
             make_qkx(x + 32 * g, w + 32 * g, 32, steps, ns, nmax, 0, &sc[g], &mn[g], L + 32 * g);
         }
@@ -747,8 +756,7 @@ static void iq4_xs_block(const float *x, const float *qw, uint8_t *out) {
 /* ------------------------------------------------------------------ */
 /* dispatch                                                            */
 /* ------------------------------------------------------------------ */
-int qs_oracle_iq(int type, const float *x, const float *qw, uint8_t *out);
-int qs_oracle_iq_supported(int type);
+#include "qs_oracle_iq.c"
 
 static int block_info(int type, int *blk, int *bytes) {
     switch (type) {

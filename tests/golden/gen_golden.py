@@ -160,16 +160,62 @@ def main() -> None:
         inputs[f"{cname}.imat"] = c["imat"]
     np.savez_compressed(Path(args.out) / "inputs.npz", **inputs)
 
+    # per-group results of the shared IQ2_XS / IQ2_S search (iq2xs_common.scale_search),
+    # recorded by wrapping the function the quantizers call
+    xs_common = importlib.import_module("kernels.iq2xs_common")
+    recorded: list = []
+
+    def recording(fn):
+        def wrapper(*a, **kw):
+            scale, win = fn(*a, **kw)
+            recorded.append((scale.clone(), win.clone()))
+            return scale, win
+        return wrapper
+
+    # and the sweep's batched projection (the first search_codes call of each
+    # scale_search): tentative codes, winning grid indices, kmap-hit flags
+    sweeps: list = []
+    reprojs: list = []
+    orig_search_codes = xs_common.search_codes
+
+    def recording_search(u_all, *a, **kw):
+        win, og = orig_search_codes(u_all, *a, **kw)
+        if kw.get("sel") is None and len(a) < 5:
+            sweeps.append((u_all.clone(), win.clone(), og.clone()))
+        else:
+            reprojs.append((u_all.clone(), kw["sel"].clone(), win.clone()))
+        return win, og
+
+    xs_common.search_codes = recording_search
+
     for tname, mod, fn, modes in TYPES:
         m = importlib.import_module(f"kernels.{mod}")
         f = getattr(m, fn)
+        if tname in ("iq2_xs", "iq2_s"):
+            m.scale_search = recording(xs_common.scale_search)
         outs = {}
         for cname, c in cases.items():
             x = torch.from_numpy(case_f32(c).copy())
             for mode in modes:
                 qw = torch.from_numpy(c["imat"].copy()) if mode == "imat" else None
+                recorded.clear()
+                sweeps.clear()
+                reprojs.clear()
                 y = f(x) if tname == "q4_0" else f(x, qw)
                 outs[f"{cname}.{mode}"] = y.numpy().astype(np.uint8)
+                if recorded:
+                    outs[f"{cname}.{mode}.search_scale"] = recorded[0][0].numpy()
+                    outs[f"{cname}.{mode}.search_win"] = recorded[0][1].numpy().astype(np.int16)
+                if sweeps:
+                    u_all, win, og = sweeps[0]
+                    outs[f"{cname}.{mode}.sweep_code"] = u_all.numpy().astype(np.uint16)
+                    outs[f"{cname}.{mode}.sweep_win"] = win.numpy().astype(np.int16)
+                    outs[f"{cname}.{mode}.sweep_on"] = og.numpy().astype(np.uint8)
+                if reprojs:
+                    u2, sel, win2 = reprojs[0]
+                    outs[f"{cname}.{mode}.reproj_code"] = u2.numpy().astype(np.uint16)
+                    outs[f"{cname}.{mode}.reproj_sel"] = sel.numpy().astype(np.uint8)
+                    outs[f"{cname}.{mode}.reproj_win"] = win2.numpy().astype(np.int16)
         np.savez_compressed(Path(args.out) / f"{tname}.npz", **outs)
         print(f"{tname}: {', '.join(f'{k}={v.shape}' for k, v in outs.items())}", flush=True)
 

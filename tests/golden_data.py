@@ -16,7 +16,8 @@ TYPES = {
     "iq2_xxs": (16, 256, 66), "iq2_xs": (17, 256, 74), "iq2_s": (22, 256, 82),
     "iq3_xxs": (18, 256, 98), "iq3_s": (21, 256, 110),
 }
-ORACLE_TYPES = ["q4_0", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_xs"]
+ORACLE_TYPES = ["q4_0", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_xs",
+                "iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs", "iq3_s"]
 
 _inputs = None
 
@@ -34,6 +35,8 @@ def cases(qtype: str):
     inp = inputs()
     out = []
     for key in sorted(g.files):
+        if key.count(".") != 1:
+            continue                      # intermediate records (e.g. search results)
         case, mode = key.split(".")
         qw = inp[f"{case}.imat"] if mode == "imat" else None
         out.append((key, inp[f"{case}.x"], qw, g[key]))
