@@ -3,12 +3,19 @@
 // they replace are in include/quant_studio.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <array>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "quant_studio.h"
+#include "qs_grids.h"
+#include "qs_iq.h"
 #include "qs_kernels.h"
 
 namespace {
@@ -58,14 +65,121 @@ const TypeInfo* find_type(int id) {
     return nullptr;
 }
 
-bool has_kernel(int id) {
-    switch (id) {
-    case QS_TYPE_Q4_0: case QS_TYPE_Q2_K: case QS_TYPE_Q3_K: case QS_TYPE_Q4_K:
-    case QS_TYPE_Q5_K: case QS_TYPE_Q6_K: case QS_TYPE_IQ4_XS:
-        return true;
-    default:
-        return false;
+bool has_kernel(int id) { return find_type(id) != nullptr; }
+
+// ---- IQ grid tables: built once per process, uploaded once per device ----
+
+enum IqTabId { IQT_G2_256, IQT_G2_512, IQT_G2_1024, IQT_G3_256, IQT_G3_512, IQT_N };
+
+struct HostTab {
+    std::vector<uint16_t> grid, nlen, nbr;
+    std::vector<int16_t> kmap;
+    std::vector<int32_t> nstart;
+};
+
+// kmap plus, for every off-grid code the level projection can produce (IQ2:
+// levels 0..2, IQ3: 0..7), the grid points within its nwant smallest distinct
+// squared distances in (distance, index) order -- the neighbour tables of
+// iq2.py:31-74, iq2xs_common.py:41-95, iq3_common.py:29-68.
+HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant) {
+    const int nsub = bits == 2 ? 8 : 4, lmask = (1 << bits) - 1, lmax = bits == 2 ? 2 : 7;
+    const int ksize = bits == 2 ? 43692 : 4096;
+    HostTab t;
+    t.grid.assign(grid, grid + gs);
+    t.kmap.assign(ksize, -1);
+    t.nstart.assign(ksize, 0);
+    t.nlen.assign(ksize, 0);
+    for (int i = 0; i < gs; i++) t.kmap[grid[i]] = (int16_t)i;
+    std::vector<int> gl(gs * nsub), d2(gs);
+    for (int i = 0; i < gs; i++)
+        for (int j = 0; j < nsub; j++) gl[i * nsub + j] = 2 * ((grid[i] >> (bits * j)) & lmask) + 1;
+    for (int c = 0; c < ksize; c++) {
+        if (t.kmap[c] >= 0) continue;
+        int p[8];
+        bool ok = true;
+        for (int j = 0; j < nsub; j++) {
+            const int l = (c >> (bits * j)) & lmask;
+            ok = ok && l <= lmax;
+            p[j] = 2 * l + 1;
+        }
+        if (!ok) continue;
+        std::vector<int> dist;
+        for (int i = 0; i < gs; i++) {
+            int s = 0;
+            for (int j = 0; j < nsub; j++) s += (p[j] - gl[i * nsub + j]) * (p[j] - gl[i * nsub + j]);
+            d2[i] = s;
+        }
+        dist.assign(d2.begin(), d2.end());
+        std::sort(dist.begin(), dist.end());
+        dist.erase(std::unique(dist.begin(), dist.end()), dist.end());
+        const int limit = dist[std::min<int>(nwant, (int)dist.size()) - 1];
+        t.nstart[c] = (int32_t)t.nbr.size();
+        for (int rank = 0; rank < (int)dist.size() && dist[rank] <= limit; rank++)
+            for (int i = 0; i < gs; i++)
+                if (d2[i] == dist[rank]) t.nbr.push_back((uint16_t)i);
+        t.nlen[c] = (uint16_t)(t.nbr.size() - t.nstart[c]);
     }
+    return t;
+}
+
+const HostTab& host_tab(int id) {
+    static std::once_flag once;
+    static std::array<HostTab, IQT_N> tabs;
+    std::call_once(once, [] {
+        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2);
+        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2);
+        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1);
+        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2);
+        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3);
+    });
+    return tabs[id];
+}
+
+std::mutex g_dev_mutex;
+std::map<int, std::array<qs::IqTabDev, IQT_N>> g_dev_tabs;
+
+template <typename T>
+const T* upload(const std::vector<T>& v) {
+    void* p = nullptr;
+    const size_t n = std::max<size_t>(1, v.size()) * sizeof(T);
+    if (hipMalloc(&p, n) != hipSuccess) return nullptr;
+    if (!v.empty() && hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+        return nullptr;
+    return static_cast<const T*>(p);
+}
+
+// Device tables of the current device (uploaded on its first IQ call; kept
+// until the process ends).
+bool device_tabs(std::array<qs::IqTabDev, IQT_N>& out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lock(g_dev_mutex);
+    auto it = g_dev_tabs.find(dev);
+    if (it == g_dev_tabs.end()) {
+        std::array<qs::IqTabDev, IQT_N> d{};
+        for (int id = 0; id < IQT_N; id++) {
+            const HostTab& h = host_tab(id);
+            d[id].grid = upload(h.grid);
+            d[id].kmap = upload(h.kmap);
+            d[id].nstart = upload(h.nstart);
+            d[id].nlen = upload(h.nlen);
+            d[id].nbr = upload(h.nbr);
+            if (!d[id].grid || !d[id].kmap || !d[id].nstart || !d[id].nlen || !d[id].nbr) return false;
+        }
+        it = g_dev_tabs.emplace(dev, d).first;
+    }
+    out = it->second;
+    return true;
+}
+
+qs::IqSteps iq_steps(float base, float delta, int lo, int hi) {
+    qs::IqSteps s{};
+    s.n = 0;
+    for (int i = lo; i <= hi; i++) {
+        float t = (float)i * delta;
+        s.v[s.n++] = base + t;
+    }
+    return s;
 }
 
 // candidate numerators, f32 chains as kq_common.py:21-30 and qx_common.py:20-23
@@ -104,7 +218,8 @@ qs::Steps qx_steps(int nmax) {
 }
 
 template <int SRC>
-void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st) {
+void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
+                 const std::array<qs::IqTabDev, IQT_N>& tabs) {
     using namespace qs;
     const unsigned sb8 = (unsigned)((a.n_units + 7) / 8), sb4 = (unsigned)((a.n_units + 3) / 4);
     switch (type) {
@@ -144,6 +259,35 @@ void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st) {
     case QS_TYPE_IQ4_XS:
         if (imat) hipLaunchKernelGGL((k_iq4_xs<SRC, true>), dim3(sb8), dim3(64), 0, st, a);
         else hipLaunchKernelGGL((k_iq4_xs<SRC, false>), dim3(sb8), dim3(64), 0, st, a);
+        break;
+    case QS_TYPE_IQ2_XXS: {
+        // candidate numerators computed in f64 and rounded once (iq2.py:387, :470)
+        QpSteps qp4{};
+        IqSteps sweep{};
+        int n = 0;
+        for (int i = -4; i <= 4; i++)
+            if (i) qp4.v[n++] = (float)(0.1 * i + 4.0);
+        for (int i = -6; i <= 6; i++) sweep.v[sweep.n++] = (float)(5.0 + 0.1 * i);
+        hipLaunchKernelGGL(k_iq2_xxs<SRC>, dim3(sb8), dim3(64), 0, st, a, tabs[IQT_G2_256], qp4, sweep);
+        break;
+    }
+    case QS_TYPE_IQ2_XS:      // SWEEP_CS iq2xs_common.py:21
+        hipLaunchKernelGGL((k_iq2_xs_s<SRC, false>), dim3(sb4), dim3(64), 0, st, a, tabs[IQT_G2_512],
+                           iq_steps(5.0f, 0.1f, -9, 9));
+        break;
+    case QS_TYPE_IQ2_S:
+        hipLaunchKernelGGL((k_iq2_xs_s<SRC, true>), dim3(sb4), dim3(64), 0, st, a, tabs[IQT_G2_1024],
+                           iq_steps(5.0f, 0.1f, -9, 9));
+        break;
+    case QS_TYPE_IQ3_XXS:     // _STEPS iq3_xxs.py:22
+        hipLaunchKernelGGL((k_iq3<SRC, false, true>), dim3(sb8), dim3(64), 0, st, a, tabs[IQT_G3_256],
+                           iq_steps(15.0f, 0.2f, -15, 15));
+        break;
+    case QS_TYPE_IQ3_S:       // _STEPS iq3_s.py:22
+        if (imat) hipLaunchKernelGGL((k_iq3<SRC, true, true>), dim3(sb8), dim3(64), 0, st, a,
+                                     tabs[IQT_G3_512], iq_steps(15.0f, 0.2f, -9, 9));
+        else hipLaunchKernelGGL((k_iq3<SRC, true, false>), dim3(sb8), dim3(64), 0, st, a,
+                                tabs[IQT_G3_512], iq_steps(15.0f, 0.2f, -9, 9));
         break;
     default:
         break;
@@ -215,11 +359,17 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     a.qw = imat ? imatrix : nullptr;
     a.dst = static_cast<uint8_t*>(dst);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    std::array<qs::IqTabDev, IQT_N> tabs{};
+    if (t->blk == 256 && (ggml_type == QS_TYPE_IQ2_XXS || ggml_type == QS_TYPE_IQ2_XS ||
+                          ggml_type == QS_TYPE_IQ2_S || ggml_type == QS_TYPE_IQ3_XXS ||
+                          ggml_type == QS_TYPE_IQ3_S)) {
+        if (!device_tabs(tabs)) return fail(QS_EIO, "%s: cannot upload grid tables to the device", t->name);
+    }
     (void)hipGetLastError();
     switch (src_type) {
-    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st); break;
-    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st); break;
-    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st); break;
+    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs); break;
+    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs); break;
+    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs); break;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(QS_EIO, "%s: launch failed: %s", t->name, hipGetErrorString(e));

@@ -1,0 +1,527 @@
+// IQ2_XXS / IQ2_XS / IQ2_S / IQ3_XXS / IQ3_S quantizer kernels (gfx950).
+//
+// One lane per group (32 values for IQ2_XXS and IQ3, 16 for IQ2_XS/S); the
+// group's candidate-scale sweep runs in registers, each step projecting the
+// group's subgroups onto the E8/3-bit grid: levels -> code -> kmap hit, or a
+// first-minimum weighted search over the code's neighbour list. Grid codes
+// (and the IQ3 kmap) are staged in LDS; the IQ2 kmaps and every neighbour
+// list are read through L1/L2 (at most 250 KB per table). Superblock scales
+// and the packed block go through LDS like the K-quant kernels.
+#pragma once
+
+#include <type_traits>
+
+#include "qs_fits.h"
+#include "qs_kernels.h"
+#include "qs_wave.h"
+
+namespace qs {
+
+// Device copy of one grid's tables (built once per device on the host).
+struct IqTabDev {
+    const uint16_t* grid;     // grid codes (BITS-bit levels per value)
+    const int16_t* kmap;      // code -> grid index, -1 when off-grid
+    const int32_t* nstart;    // code -> first neighbour in nbr
+    const uint16_t* nlen;     // code -> neighbour count (off-grid codes)
+    const uint16_t* nbr;      // neighbour grid indices, (distance, index) order
+};
+
+template <int I, int END, typename F>
+QS_DEV void static_for(F&& f) {
+    if constexpr (I < END) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, END>(f);
+    }
+}
+
+template <int BITS>
+QS_DEV float grid_value(uint32_t gcode, int j) {
+    return (float)(2 * ((gcode >> (BITS * j)) & ((1u << BITS) - 1u)) + 1);
+}
+
+// Project one subgroup (values OFF..OFF+NV-1 of the lane's group) at the
+// candidate scale: levels clamp(round(0.5*(inv*x - 1)), 0, LMAX), then the
+// kmap, then the first-minimum weighted distance over the neighbour list
+// (iq2.py:347-372, iq2xs_common.py:222-271, iq3_common.py:209-256).
+// IQ2 distances are a left-to-right sum of 8 terms from +0; IQ3's are
+// ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and diff = sc*g - x.
+template <int BITS, int NV, int OFF, int N>
+QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const int16_t* kmap_lds,
+                      const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool& on) {
+    constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
+    int code = 0;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        float t = inv * xv[OFF + j];
+        t = t - 1.0f;
+        t = 0.5f * t;
+        code |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
+    }
+    const int g = kmap_lds ? (int)kmap_lds[code] : (int)T.kmap[code];
+    on = g >= 0;
+    if (g >= 0) return g;
+    const int st = T.nstart[code], n = T.nlen[code];
+    float best = __builtin_inff();
+    int bi = -1;
+    for (int k = 0; k < n; k++) {
+        const int gi = T.nbr[st + k];
+        const uint32_t gc = glds[gi];
+        float d2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            float diff = sc * grid_value<BITS>(gc, j);
+            diff = diff - xv[OFF + j];
+            const float t = (wv[OFF + j] * diff) * diff;
+            if constexpr (NV == 4) d2 = (j == 0) ? t : d2 + t;
+            else d2 = d2 + t;
+        }
+        if (d2 < best) {
+            best = d2;
+            bi = gi;
+        }
+    }
+    return bi;
+}
+
+// sign-parity fold of 8 values (iq2.py:438-450): |x|, the smallest (w*x)*x
+// entry negated when the sign count is odd; returns the 7 stored sign bits
+template <int OFF, int N>
+QS_DEV int parity_fold8(const float (&x)[N], const float (&w)[N], float (&xval)[N]) {
+    int s = 0, nneg = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        xval[OFF + j] = fabsf(x[OFF + j]);
+        const bool neg = x[OFF + j] < 0;
+        s |= neg ? (1 << j) : 0;
+        nneg += neg ? 1 : 0;
+    }
+    float m = (w[OFF] * x[OFF]) * x[OFF];
+    int imin = 0;
+#pragma unroll
+    for (int j = 1; j < 8; j++) {
+        const float v = (w[OFF + j] * x[OFF + j]) * x[OFF + j];
+        const bool lt = v < m;
+        m = lt ? v : m;
+        imin = lt ? j : imin;
+    }
+    const bool odd = nneg & 1;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (odd && imin == j) xval[OFF + j] = -xval[OFF + j];
+    s ^= odd ? (1 << imin) : 0;
+    return s & 127;
+}
+
+template <int OFF, int N>
+QS_DEV int sign_bits8(const float (&x)[N], float (&xval)[N]) {
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        xval[OFF + j] = fabsf(x[OFF + j]);
+        s |= x[OFF + j] < 0 ? (1 << j) : 0;
+    }
+    return s;
+}
+
+// sums of (w*xval)*q and (w*q)*q over the lane's group for grid winners gi[]
+template <int BITS, int NV, int NSUB, int N>
+QS_DEV void iq_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
+                    float (&a)[N], float (&b)[N]) {
+#pragma unroll
+    for (int s = 0; s < NSUB; s++) {
+        const uint32_t gc = glds[gi[s]];
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const float q = grid_value<BITS>(gc, j);
+            a[NV * s + j] = (w[NV * s + j] * xval[NV * s + j]) * q;
+            b[NV * s + j] = (w[NV * s + j] * q) * q;
+        }
+    }
+}
+
+// superblock scale nibbles: d = max/31, l = clamp(round(0.5*(sc/d - 1)), 0, 15)
+// (iq2.py:92-96, iq2xs_common.py:345-355, iq3_xxs.py:115-121)
+template <int NG>
+QS_DEV void iq_scale_nibbles(const float* sc, float& d, bool& has, int (&l)[NG]) {
+    float mx = sc[0];
+#pragma unroll
+    for (int i = 1; i < NG; i++) mx = fmaxf(mx, sc[i]);
+    has = mx > 0;
+    d = mx / 31.0f;
+    const float inv_d = 1.0f / (has ? d : 1.0f);
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        float t = inv_d * sc[i];
+        t = t - 1.0f;
+        t = 0.5f * t;
+        l[i] = (int)clampf(rintf(t), 0.0f, 15.0f);
+    }
+}
+
+struct IqSteps {
+    float v[32];
+    int n;
+};
+
+template <int SRC, int LPS, int GROUP>
+QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float* vlds, float* tmp, float sig_mult,
+                            bool use_x2, float (&x)[GROUP], float (&w)[GROUP]) {
+    load_elems<SRC, true, GROUP>(a.src, p.elem, x);
+    if (use_x2) {
+#pragma unroll
+        for (int i = 0; i < GROUP; i++) w[i] = x[i] * x[i];
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < GROUP; i++) vlds[GROUP * p.g + i] = x[i] * x[i];
+    wave_sync();
+    const float sum = sb_cascade8_256<LPS>(vlds, tmp, p.g);
+    const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
+#pragma unroll
+    for (int i = 0; i < GROUP; i++) {
+        const float t = x[i] * x[i];
+        w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
+    }
+}
+
+// ------------------------------------------------------------------
+// IQ2_XXS  quantize_iq2_xxs iq2.py:418-498 (+ _finalize :87-108)
+// ------------------------------------------------------------------
+template <int SRC>
+__global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4, IqSteps sweep) {
+    constexpr int LPS = 8, SPW = 8, BYTES = 66;
+    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ uint16_t glds[256];
+    for (int i = threadIdx.x; i < 256; i += 64) glds[i] = T.grid[i];
+    const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[32], w[32], waux[32], xval[32];
+    iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 1.0f, false, x, w);
+#pragma unroll
+    for (int i = 0; i < 32; i++) waux[i] = sqrtf(w[i]);
+    int signs[4];
+    static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
+    float gmax = xval[0];
+#pragma unroll
+    for (int i = 1; i < 32; i++) gmax = fmaxf(gmax, xval[i]);
+    bool active = gmax >= GROUP_MAX_EPS;
+    float Lq[32];
+    const float scale0 = qp_fit<32>(xval, w, 4, qp4.v, Lq);
+    const float eff = scale0 * 3.0f;
+    active = active && eff > 0;
+    const float eff_safe = active ? eff : 1.0f;
+    float scale = scale0, best = 0.0f;
+    const int zero_gi = T.kmap[0] >= 0 ? T.kmap[0] : 0;
+    int L[4] = {zero_gi, zero_gi, zero_gi, zero_gi};
+    float ta[32], tb[32];
+#pragma unroll 1
+    for (int st = 0; st < sweep.n; st++) {
+        const float inv = rdiv(sweep.v[st], eff_safe);
+        const float sc = 1.0f / inv;
+        int gi[4];
+        bool on;
+        static_for<0, 4>([&](auto S) { gi[S] = iq_project<2, 8, 8 * S>(T, glds, nullptr, xval, waux, inv, sc, on); });
+        iq_sums<2, 8, 4>(glds, gi, w, xval, ta, tb);
+        const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
+        if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            const float ns = sumqx / fmaxf(sumq2, F32_TINY);
+            scale = ns;
+            best = ns * sumqx;
+#pragma unroll
+            for (int k = 0; k < 4; k++) L[k] = gi[k];
+        }
+    }
+    const bool proj = active && scale > 0;
+    {
+        const float inv = 1.0f / (proj ? scale : 1.0f);
+        int gp[4];
+        bool on;
+        static_for<0, 4>([&](auto S) { gp[S] = iq_project<2, 8, 8 * S>(T, glds, nullptr, xval, waux, inv, scale, on); });
+        iq_sums<2, 8, 4>(glds, gp, w, xval, ta, tb);
+        const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
+        if (proj && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
+        if (proj) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) L[k] = gp[k];
+        }
+    }
+    if (active && scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 4; k++) signs[k] = (~signs[k]) & 127;
+    }
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        lo |= (uint32_t)L[k] << (8 * k);
+        hi |= (uint32_t)signs[k] << (7 * k);
+    }
+    s.sc[slot][g] = active ? scale : 0.0f;
+    wave_sync();
+    float d;
+    bool has;
+    int l[8];
+    iq_scale_nibbles<8>(s.sc[slot], d, has, l);
+    const uint32_t wlo = (active && has) ? lo : 0u;
+    const uint32_t whi = has ? ((active ? hi : 0u) | ((uint32_t)l[g] << 28)) : 0u;
+    uint8_t* o = s.out + slot * BYTES;
+    if (g == 0) {
+        const uint32_t h = f16_bits(has ? d : 0.0f);
+        o[0] = (uint8_t)h;
+        o[1] = (uint8_t)(h >> 8);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        o[2 + 8 * g + k] = (uint8_t)(wlo >> (8 * k));
+        o[2 + 8 * g + 4 + k] = (uint8_t)(whi >> (8 * k));
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// IQ2_XS / IQ2_S  scale_search iq2xs_common.py:280-342; quantize_iq2_xs
+// iq2_xs.py:20-69; quantize_iq2_s iq2_s.py:21-62
+// ------------------------------------------------------------------
+template <int SRC, bool IS_S>
+__global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
+    constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 82 : 74, GS = IS_S ? 1024 : 512;
+    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ uint16_t glds[GS];
+    __shared__ int wlds[SPW][16][2];
+    for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
+    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[16], w[16], waux[16], xval[16];
+    iq_load_weights<SRC, LPS, 16>(a, p, s.v[slot], s.tmp[slot], IS_S ? 2.0f : 1.0f, false, x, w);
+#pragma unroll
+    for (int i = 0; i < 16; i++) waux[i] = sqrtf(w[i]);
+    int signs[2];
+    if constexpr (IS_S) {
+        signs[0] = sign_bits8<0>(x, xval);
+        signs[1] = sign_bits8<8>(x, xval);
+    } else {
+        signs[0] = parity_fold8<0>(x, w, xval);
+        signs[1] = parity_fold8<8>(x, w, xval);
+    }
+    float gmax = xval[0];
+#pragma unroll
+    for (int i = 1; i < 16; i++) gmax = fmaxf(gmax, xval[i]);
+    const bool active = IS_S ? gmax >= 1e-8f : gmax >= GROUP_MAX_EPS;
+    const float gsafe = active ? gmax : 1.0f;
+    const int code0 = T.kmap[0] >= 0 ? T.kmap[0] : 0;
+    float scale = active ? gmax / 5.0f : 0.0f, best = 0.0f;
+    int win[2] = {code0, code0};
+    bool og[2] = {true, true};
+    float ta[16], tb[16];
+#pragma unroll 1
+    for (int st = 0; st < sweep.n; st++) {
+        const float inv = rdiv(sweep.v[st], gsafe), sc = 1.0f / inv;
+        int gi[2];
+        bool on[2];
+        gi[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, sc, on[0]);
+        gi[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, sc, on[1]);
+        iq_sums<2, 8, 2>(glds, gi, w, xval, ta, tb);
+        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            const float ns = sumqx / fmaxf(sumq2, F32_TINY);
+            scale = ns;
+            best = ns * sumqx;
+            win[0] = gi[0];
+            win[1] = gi[1];
+            og[0] = on[0];
+            og[1] = on[1];
+        }
+    }
+    const bool need = active && scale > 0 && !(og[0] && og[1]);
+    if (need) {
+        const float inv = 1.0f / scale;
+        bool on;
+        if (!og[0]) win[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, scale, on);
+        if (!og[1]) win[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, scale, on);
+        iq_sums<2, 8, 2>(glds, win, w, xval, ta, tb);
+        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        if (sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
+    }
+    if (active && scale < 0) {
+        scale = -scale;
+        signs[0] = (~signs[0]) & (IS_S ? 255 : 127);
+        signs[1] = (~signs[1]) & (IS_S ? 255 : 127);
+    }
+    s.sc[slot][g] = active ? scale : 0.0f;
+    wlds[slot][g][0] = active ? win[0] : 0;
+    wlds[slot][g][1] = active ? win[1] : 0;
+    wave_sync();
+    float d;
+    bool has;
+    int l[16];
+    iq_scale_nibbles<16>(s.sc[slot], d, has, l);
+    uint8_t* o = s.out + slot * BYTES;
+    if constexpr (!IS_S) {
+        if (g == 0) {
+            const uint32_t h = f16_bits(has ? d : 0.0f);
+            o[0] = (uint8_t)h;
+            o[1] = (uint8_t)(h >> 8);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t q2 = (active && has) ? ((uint32_t)win[k] | ((uint32_t)signs[k] << 9)) : 0u;
+            o[2 + 4 * g + 2 * k] = (uint8_t)q2;
+            o[2 + 4 * g + 2 * k + 1] = (uint8_t)(q2 >> 8);
+        }
+        if (g < 8) o[66 + g] = (uint8_t)(has ? (l[2 * g] | (l[2 * g + 1] << 4)) : 0);
+    } else {
+        if (g == 0) {
+            const uint32_t h = f16_bits(has ? d * 0.9875f : 0.0f);
+            o[0] = (uint8_t)h;
+            o[1] = (uint8_t)(h >> 8);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            o[2 + 2 * g + k] = (uint8_t)((active ? win[k] : 0) & 255);
+            o[34 + 2 * g + k] = (uint8_t)(active ? signs[k] : 0);
+        }
+        if (g < 8) {
+            int v = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int sub = 4 * g + t;
+                v |= (wlds[slot][sub >> 1][sub & 1] >> 8) << (2 * t);
+            }
+            o[66 + g] = (uint8_t)v;
+            o[74 + g] = (uint8_t)(has ? (l[2 * g] | (l[2 * g + 1] << 4)) : 0);
+        }
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// IQ3_XXS / IQ3_S  quantize_iq3_xxs iq3_xxs.py:31-134, quantize_iq3_s
+// iq3_s.py:31-140
+// ------------------------------------------------------------------
+template <int SRC, bool IS_S, bool IMAT>
+__global__ __launch_bounds__(64) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
+    constexpr int LPS = 8, SPW = 8, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
+    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ uint16_t glds[GS];
+    __shared__ int16_t klds[4096];
+    __shared__ int act_lds[SPW][8];
+    for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
+    for (int i = threadIdx.x; i < 4096; i += 64) klds[i] = T.kmap[i];
+    const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, g = p.g;
+    float x[32], w[32], waux[32], xval[32];
+    iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 2.0f, !IMAT, x, w);
+#pragma unroll
+    for (int i = 0; i < 32; i++) waux[i] = sqrtf(w[i]);
+    int signs[4];
+    if constexpr (IS_S) {
+        static_for<0, 4>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });
+    } else {
+        static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
+    }
+    float gmax = xval[0];
+#pragma unroll
+    for (int i = 1; i < 32; i++) gmax = fmaxf(gmax, xval[i]);
+    const bool active = IS_S ? gmax > 0 : gmax >= 1e-8f;
+    const float gsafe = active ? gmax : 1.0f;
+    float scale = gmax / 15.0f, best = 0.0f;
+    int Wg[8];
+    bool og[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        Wg[k] = 0;
+        og[k] = !IS_S;
+    }
+    float ta[32], tb[32];
+    wave_sync();   // glds / klds ready
+#pragma unroll 1
+    for (int st = 0; st < steps.n; st++) {
+        const float inv = rdiv(steps.v[st], gsafe), sc = 1.0f / inv;
+        int gi[8];
+        bool on[8];
+        static_for<0, 8>([&](auto S) { gi[S] = iq_project<3, 4, 4 * S>(T, glds, klds, xval, waux, inv, sc, on[S]); });
+        iq_sums<3, 4, 8>(glds, gi, w, xval, ta, tb);
+        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
+            const float ns = sumqx / fmaxf(sumq2, F32_TINY);
+            scale = ns;
+            best = ns * sumqx;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                Wg[k] = gi[k];
+                og[k] = on[k];
+            }
+        }
+    }
+    bool anyoff = false;
+#pragma unroll
+    for (int k = 0; k < 8; k++) anyoff = anyoff || !og[k];
+    const bool redo = active && anyoff && scale > 0;
+    {
+        const float inv2 = 1.0f / (redo ? scale : 1.0f);
+        int w2[8];
+        bool on[8];
+        static_for<0, 8>([&](auto S) { w2[S] = iq_project<3, 4, 4 * S>(T, glds, klds, xval, waux, inv2, scale, on[S]); });
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (redo && (IS_S || !og[k])) Wg[k] = w2[k];
+        iq_sums<3, 4, 8>(glds, Wg, w, xval, ta, tb);
+        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        if (redo && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
+    }
+    if (active && scale < 0) {
+        scale = -scale;
+#pragma unroll
+        for (int k = 0; k < 4; k++) signs[k] = (~signs[k]) & (IS_S ? 255 : 127);
+    }
+    s.sc[slot][g] = active ? scale : 0.0f;
+    act_lds[slot][g] = active ? 1 : 0;
+    uint8_t* o = s.out + slot * BYTES;
+    for (int t = g; t < BYTES; t += LPS) o[t] = 0;
+    wave_sync();
+    float d;
+    bool has;
+    int l[8];
+    iq_scale_nibbles<8>(s.sc[slot], d, has, l);
+    if constexpr (!IS_S) {
+        if (g == 0) {
+            const uint32_t h = f16_bits(has ? d * 1.0125f : 0.0f);
+            o[0] = (uint8_t)h;
+            o[1] = (uint8_t)(h >> 8);
+        }
+        uint32_t word = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) word |= (uint32_t)(active ? signs[k] : 0) << (7 * k);
+        word |= (uint32_t)l[g] << 28;
+        if (!has) word = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) o[2 + 8 * g + k] = (uint8_t)((has && active) ? Wg[k] : 0);
+#pragma unroll
+        for (int k = 0; k < 4; k++) o[66 + 4 * g + k] = (uint8_t)(word >> (8 * k));
+    } else {
+        if (g == 0) {
+            const uint32_t h = f16_bits(has ? d * 1.033f : 0.0f);
+            o[0] = (uint8_t)h;
+            o[1] = (uint8_t)(h >> 8);
+        }
+        int h = 0;
+#pragma unroll
+        for (int k = 0; k < 8; k++) h |= (Wg[k] >> 8) << k;
+        o[66 + g] = (uint8_t)(active ? h : 0);
+        if (active) {
+            int slot_idx = 0;                  // live groups compact to the front (iq3_s.py:113-122)
+            for (int j = 0; j < g; j++) slot_idx += act_lds[slot][j];
+#pragma unroll
+            for (int k = 0; k < 8; k++) o[2 + 8 * slot_idx + k] = (uint8_t)(Wg[k] & 255);
+#pragma unroll
+            for (int k = 0; k < 4; k++) o[74 + 4 * slot_idx + k] = (uint8_t)signs[k];
+        }
+        if (g < 4) o[106 + g] = (uint8_t)(has ? (l[2 * g] | (l[2 * g + 1] << 4)) : 0);
+    }
+    wave_sync();
+    sb_store(s, a);
+}
+
+}  // namespace qs

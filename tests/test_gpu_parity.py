@@ -15,7 +15,9 @@ from golden_data import TYPES, block_identical, cases
 
 pytestmark = pytest.mark.gpu
 
-HIP_TYPES = ["q4_0", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_xs"]
+HIP_TYPES = ["q4_0", "q2_k", "q3_k", "q4_k", "q5_k", "q6_k", "iq4_xs",
+             "iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs", "iq3_s"]
+NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
 NTHREADS = min(16, len(os.sched_getaffinity(0)))
 
 
@@ -75,6 +77,8 @@ def c2_like(rows: int, k: int, seed: int):
 def test_oracle_parity_random(qs, dev, qtype, imat):
     if qtype == "q4_0" and imat:
         pytest.skip("Q4_0 ignores an imatrix")
+    if qtype in NEEDS_IMATRIX and not imat:
+        pytest.skip(f"{qtype} requires an imatrix")
     x, qw = c2_like(384, 2560, seed=sum(map(ord, qtype)) * 2 + int(imat))
     qw = qw if imat else None
     print(f"{qtype} imat={imat} 384x2560", flush=True)
@@ -110,7 +114,7 @@ def test_q4_k_imatrix_full_ffn_shapes(qs, dev):
         assert same.all(), f"{rows}x{k}: {int((~same).sum())}/{same.size} blocks differ"
 
 
-@pytest.mark.parametrize("qtype", ["q4_0", "q4_k", "q6_k", "q3_k"])
+@pytest.mark.parametrize("qtype", ["q4_0", "q4_k", "q6_k", "q3_k", "iq2_xxs", "iq2_s", "iq3_s"])
 def test_row_chunking_invariance(qs, dev, qtype):
     x, qw = c2_like(300, 1024, seed=9)
     tid = TYPES[qtype][0]
@@ -122,7 +126,7 @@ def test_row_chunking_invariance(qs, dev, qtype):
     assert torch.equal(whole, parts)
 
 
-@pytest.mark.parametrize("qtype", ["q4_0", "q5_k", "q2_k", "iq4_xs"])
+@pytest.mark.parametrize("qtype", ["q4_0", "q5_k", "q2_k", "iq4_xs", "iq2_xs", "iq3_xxs"])
 def test_f16_source(qs, dev, qtype):
     rng = np.random.default_rng(4)
     a = (rng.standard_normal((64, 512)) * 0.05).astype(np.float16)
@@ -139,7 +143,7 @@ def test_row_stride_and_unaligned_output(qs, dev):
     wide[:, :1024] = to_device(x, dev)
     view = wide[:, :1024]                       # row stride 1088 elements (2176 B)
     assert view.stride(0) == 1088
-    for qtype in ("q4_0", "q6_k", "q4_k"):
+    for qtype in ("q4_0", "q6_k", "q4_k", "iq2_xxs", "iq3_s"):
         tid = TYPES[qtype][0]
         rb = TYPES[qtype][2] * (1024 // TYPES[qtype][1])
         buf = torch.zeros(40 * rb + 3, dtype=torch.uint8, device=dev)
