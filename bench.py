@@ -32,8 +32,11 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 # output bytes per 256 input values (per 32 for Q4_0 -> scaled to 256)
 OUT_BYTES_PER_256 = {"q4_0": 144, "q2_k": 84, "q3_k": 110, "q4_k": 144, "q5_k": 176,
-                     "q6_k": 210, "iq4_xs": 136}
-TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14, "iq4_xs": 23}
+                     "q6_k": 210, "iq4_xs": 136, "iq2_xxs": 66, "iq2_xs": 74, "iq2_s": 82,
+                     "iq3_xxs": 98, "iq3_s": 110}
+TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14, "iq4_xs": 23,
+            "iq2_xxs": 16, "iq2_xs": 17, "iq2_s": 22, "iq3_xxs": 18, "iq3_s": 21}
+NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
 SHAPES = [(9728, 2560), (2560, 9728)]   # (rows, k)
 ROTATE_BYTES = 1 << 30
 
@@ -200,7 +203,8 @@ def main() -> int:
     sel = [] if args.types == "none" else (list(TYPE_IDS) if args.types == "all"
                                            else args.types.split(","))
     for qtype in sel:
-        for imat in ((False,) if qtype == "q4_0" else (False, True)):
+        modes = (False,) if qtype == "q4_0" else (True,) if qtype in NEEDS_IMATRIX else (False, True)
+        for imat in modes:
             st, km = time_type(torch, qs, qtype, imat, xs_rot, qws, outs_for(qtype),
                                max(3, args.steps // 4), 1)
             a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
