@@ -32,7 +32,9 @@ struct QpSteps {
 // ------------------------------------------------------------------
 // Q4_0  (q4_0.py:14-33)
 // ------------------------------------------------------------------
-constexpr int Q40_BLOCKS_PER_WG = 64;  // 256 threads, 4 lanes per block
+constexpr int Q40_TILE = 64;                   // blocks per 256-thread tile (4 lanes per block)
+constexpr int Q40_TILES = 4;                   // tiles per workgroup, loaded before any compute
+constexpr int Q40_BLOCKS_PER_WG = Q40_TILE * Q40_TILES;
 
 template <int SRC>
 __global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
@@ -40,63 +42,83 @@ __global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
     const int tid = threadIdx.x;
     const int q = tid & 3;                       // quarter of the block: values 8q..8q+7
     const int64_t b0 = (int64_t)blockIdx.x * Q40_BLOCKS_PER_WG;
-    int64_t b = b0 + (tid >> 2);
-    const bool valid = b < a.n_units;
-    b = valid ? b : a.n_units - 1;
-    const int64_t row = b / a.units_per_row;
-    const int64_t col = (b % a.units_per_row) * 32 + 8 * q;
-    float x[8];
-    load_elems<SRC, true, 8>(a.src, row * a.stride + col, x);
-
-    // signed value of the largest |x|, first index wins (argmax of abs)
-    float am = fabsf(x[0]), mv = x[0];
-    int idx = 8 * q;
+    float x[Q40_TILES][8];
+    // issue every tile's 16-byte loads first: 16 KB of bf16 in flight per workgroup
 #pragma unroll
-    for (int i = 1; i < 8; i++) {
-        const float v = fabsf(x[i]);
-        const bool gt = v > am;
-        am = gt ? v : am;
-        mv = gt ? x[i] : mv;
-        idx = gt ? 8 * q + i : idx;
+    for (int u = 0; u < Q40_TILES; u++) {
+        int64_t b = b0 + u * Q40_TILE + (tid >> 2);
+        b = b < a.n_units ? b : a.n_units - 1;
+        const int64_t row = b / a.units_per_row;
+        const int64_t col = (b % a.units_per_row) * 32 + 8 * q;
+        load_elems<SRC, true, 8>(a.src, row * a.stride + col, x[u]);
     }
 #pragma unroll
-    for (int m = 1; m <= 2; m <<= 1) {
-        const float pam = __shfl_xor(am, m, 4);
-        const float pmv = __shfl_xor(mv, m, 4);
-        const int pidx = __shfl_xor(idx, m, 4);
-        const bool take = pam > am || (pam == am && pidx < idx);
-        am = take ? pam : am;
-        mv = take ? pmv : mv;
-        idx = take ? pidx : idx;
-    }
-    const float d = mv / -8.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t nib = 0;
+    for (int u = 0; u < Q40_TILES; u++) {
+        // signed value of the largest |x|, first index wins (argmax of abs)
+        float am = fabsf(x[u][0]), mv = x[u][0];
+        int idx = 8 * q;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        float t = x[i] * id;
-        t = t + 8.5f;
-        const uint32_t qv = (uint32_t)clampf(floorf(t), 0.0f, 15.0f);
-        nib |= qv << (4 * i);
-    }
-    // qs[j] = q[j] | q[j+16] << 4: quarters 0/1 take the high nibbles of 2/3
-    const uint32_t hi = __shfl_xor(nib, 2, 4);
-    uint8_t* o = stage + (tid >> 2) * 18;
-    if (q == 0) {
-        const uint32_t h = f16_bits(d);
-        o[0] = (uint8_t)h;
-        o[1] = (uint8_t)(h >> 8);
-    }
-    if (q < 2) {
+        for (int i = 1; i < 8; i++) {
+            const float v = fabsf(x[u][i]);
+            const bool gt = v > am;
+            am = gt ? v : am;
+            mv = gt ? x[u][i] : mv;
+            idx = gt ? 8 * q + i : idx;
+        }
 #pragma unroll
-        for (int i = 0; i < 8; i++)
-            o[2 + 8 * q + i] = (uint8_t)(((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4));
+        for (int m = 1; m <= 2; m <<= 1) {
+            const float pam = __shfl_xor(am, m, 4);
+            const float pmv = __shfl_xor(mv, m, 4);
+            const int pidx = __shfl_xor(idx, m, 4);
+            const bool take = pam > am || (pam == am && pidx < idx);
+            am = take ? pam : am;
+            mv = take ? pmv : mv;
+            idx = take ? pidx : idx;
+        }
+        const float d = mv / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t nib = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float t = x[u][i] * id;
+            t = t + 8.5f;
+            const uint32_t qv = (uint32_t)clampf(floorf(t), 0.0f, 15.0f);
+            nib |= qv << (4 * i);
+        }
+        // qs[j] = q[j] | q[j+16] << 4: quarters 0/1 take the high nibbles of 2/3
+        const uint32_t hi = __shfl_xor(nib, 2, 4);
+        uint8_t* o = stage + (u * Q40_TILE + (tid >> 2)) * 18;
+        if (q == 0) {
+            const uint32_t h = f16_bits(d);
+            o[0] = (uint8_t)h;
+            o[1] = (uint8_t)(h >> 8);
+        }
+        if (q < 2) {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                w0 |= (((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4)) << (8 * i);
+                w1 |= (((nib >> (4 * (i + 4))) & 15u) | (((hi >> (4 * (i + 4))) & 15u) << 4)) << (8 * i);
+            }
+            // 2-byte aligned destination: four 16-bit LDS stores
+            uint16_t* o16 = reinterpret_cast<uint16_t*>(o + 2 + 8 * q);
+            o16[0] = (uint16_t)w0;
+            o16[1] = (uint16_t)(w0 >> 16);
+            o16[2] = (uint16_t)w1;
+            o16[3] = (uint16_t)(w1 >> 16);
+        }
     }
     __syncthreads();
     const int64_t nvalid = min((int64_t)Q40_BLOCKS_PER_WG, a.n_units - b0);
     const int nbytes = (int)nvalid * 18;
     uint8_t* dbase = a.dst + b0 * 18;
-    if ((reinterpret_cast<uintptr_t>(dbase) & 3) == 0) {
+    if ((reinterpret_cast<uintptr_t>(dbase) & 15) == 0) {
+        const int n16 = nbytes >> 4;
+        const uint4* s16 = reinterpret_cast<const uint4*>(stage);
+        uint4* d16 = reinterpret_cast<uint4*>(dbase);
+        for (int t = tid; t < n16; t += 256) d16[t] = s16[t];
+        for (int t = (n16 << 4) + tid; t < nbytes; t += 256) dbase[t] = stage[t];
+    } else if ((reinterpret_cast<uintptr_t>(dbase) & 3) == 0) {
         const int nw = nbytes >> 2;
         const uint32_t* s4 = reinterpret_cast<const uint32_t*>(stage);
         uint32_t* d4 = reinterpret_cast<uint32_t*>(dbase);
