@@ -42,6 +42,10 @@ class GGMLQuantizationType(enum.IntEnum):
     TQ1_0 = 34
     TQ2_0 = 35
     MXFP4 = 39
+    # named by the scheme table only; not in the public type table this build
+    # restates, so they get ids outside it
+    Q1_0 = 100
+    Q2_0 = 101
 
 
 class LlamaFileType(enum.IntEnum):
@@ -78,3 +82,19 @@ class LlamaFileType(enum.IntEnum):
     MOSTLY_TQ1_0 = 36
     MOSTLY_TQ2_0 = 37
     MOSTLY_MXFP4_MOE = 38
+    MOSTLY_Q1_0 = 100
+    MOSTLY_Q2_0 = 101
+
+
+_T = GGMLQuantizationType
+# (values per block, bytes per block): the public GGML type table
+QUANT_SIZES: dict[GGMLQuantizationType, tuple[int, int]] = {
+    _T.F32: (1, 4), _T.F16: (1, 2), _T.Q4_0: (32, 18), _T.Q4_1: (32, 20), _T.Q5_0: (32, 22),
+    _T.Q5_1: (32, 24), _T.Q8_0: (32, 34), _T.Q8_1: (32, 36), _T.Q2_K: (256, 84),
+    _T.Q3_K: (256, 110), _T.Q4_K: (256, 144), _T.Q5_K: (256, 176), _T.Q6_K: (256, 210),
+    _T.Q8_K: (256, 292), _T.IQ2_XXS: (256, 66), _T.IQ2_XS: (256, 74), _T.IQ3_XXS: (256, 98),
+    _T.IQ1_S: (256, 50), _T.IQ4_NL: (32, 18), _T.IQ3_S: (256, 110), _T.IQ2_S: (256, 82),
+    _T.IQ4_XS: (256, 136), _T.I8: (1, 1), _T.I16: (1, 2), _T.I32: (1, 4), _T.I64: (1, 8),
+    _T.F64: (1, 8), _T.IQ1_M: (256, 56), _T.BF16: (1, 2), _T.TQ1_0: (256, 54),
+    _T.TQ2_0: (256, 66), _T.MXFP4: (32, 17), _T.Q1_0: (128, 18), _T.Q2_0: (64, 18),
+}
