@@ -1,0 +1,125 @@
+"""CPU tests of the GGUF container I/O and the command line (plan, dry run,
+error paths) -- the parts of the drop-in that need no GPU."""
+
+from __future__ import annotations
+
+import importlib
+import struct
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from cli_models import GT, KV, VT, imatrix_for, io, small_model
+
+ROOT = Path(__file__).resolve().parent.parent
+CLI = [sys.executable, str(ROOT / "quant-studio.py")]
+
+
+def run_cli(*args, check=True):
+    r = subprocess.run([*CLI, *map(str, args)], capture_output=True, text=True, timeout=300)
+    if check and r.returncode != 0:
+        raise AssertionError(f"exit {r.returncode}: {r.stderr}")
+    return r
+
+
+def test_header_bytes_follow_the_format(tmp_path):
+    p = tmp_path / "t.gguf"
+    io.write_gguf(p, "llama", [KV("a.b", VT.UINT32, 7)],
+                  [("w", (4, 2), GT.F32, np.arange(8, dtype=np.float32).reshape(2, 4))])
+    b = p.read_bytes()
+    assert b[:4] == b"GGUF" and struct.unpack_from("<IQQ", b, 4) == (3, 1, 2)
+    off = 24
+    key_len = struct.unpack_from("<Q", b, off)[0]
+    assert b[off + 8:off + 8 + key_len] == b"general.architecture"     # written first
+    r = io.GGUFReader(p)
+    assert list(r.kv) == ["general.architecture", "a.b"]
+    t = r.tensors[0]
+    assert (t.name, t.ne, t.ggml_type, t.offset) == ("w", (4, 2), GT.F32, 0)
+    assert r.data_offset % 32 == 0 and len(b) % 32 == 0
+    assert np.array_equal(t.array(), np.arange(8, dtype=np.float32).reshape(2, 4))
+
+
+def test_roundtrip_every_value_type(tmp_path):
+    p = tmp_path / "m.gguf"
+    small_model(p)
+    r = io.GGUFReader(p)
+    q = tmp_path / "copy.gguf"
+    io.write_gguf(q, r.get("general.architecture"),
+                  [kv for n, kv in r.kv.items() if n != "general.architecture"],
+                  [(t.name, t.ne, t.ggml_type, t.data) for t in r.tensors])
+    assert q.read_bytes() == p.read_bytes()
+    assert r.get("tokenizer.ggml.tokens") == ["<s>", "</s>", "hello"]
+    assert r.get("test.flag") is True and r.get("test.i64") == -(1 << 40)
+    assert r.get("llama.attention.layer_norm_rms_epsilon") == np.float32(1e-5)
+
+
+def test_imatrix_loader_divides_by_counts(tmp_path):
+    p = tmp_path / "im.gguf"
+    vals = imatrix_for(p, {"a.weight": 64, "b.weight": 32}, n_mat={"b.weight": 3})
+    got = io.load_imatrix(p)
+    assert set(got) == {"a.weight", "b.weight"}
+    np.testing.assert_array_equal(got["a.weight"], vals["a.weight"])
+    assert got["b.weight"].shape == (96,)
+
+
+def test_dry_run_plan(tmp_path):
+    src = tmp_path / "in.gguf"
+    small_model(src)
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--dry-run")
+    lines = {ln.split()[0]: ln.split() for ln in r.stdout.splitlines() if ln.startswith(("blk", "tok", "rope"))}
+    assert lines["blk.0.attn_q.weight"][1:4] == ["F32", "->", "Q4_0"]
+    assert lines["blk.0.attn_norm.weight"][3] == "F32"          # 1-D: passthrough
+    assert lines["blk.0.odd.weight"][3] == "F32"                # 40 % 32: Q4_0 has no fallback
+    assert "dry run:" in r.stdout
+    assert "no tensor type fallback" in r.stderr
+
+
+@pytest.mark.parametrize("argv,msg", [
+    (["q4_0", "--allow-requantize"], "--allow-requantize is not supported"),
+    (["q4_0", "--keep-split"], "--keep-split is not supported"),
+    (["NOPE"], "unknown quantization scheme"),
+    (["Q8_0"], "not supported by quant-studio"),
+    (["q4_0", "8"], "nthreads argument is not supported"),
+    (["iq2_xxs"], "require importance matrix data"),
+    (["q4_0", "--tensor-type", "attn"], "expected name=ggml_type"),
+    (["q4_0", "--token-embedding-type", "q9_9"], "unknown ggml type"),
+    (["q4_0", "--device", "cpu"], "ROCm devices only"),
+])
+def test_cli_errors(tmp_path, argv, msg):
+    src = tmp_path / "in.gguf"
+    small_model(src, odd=False)
+    args = [src] + ([tmp_path / "o.gguf"] if argv[0] != "q4_0" or "8" not in argv else []) + argv
+    if argv == ["q4_0", "8"]:
+        args = [src, "q4_0", "8"]
+    r = run_cli(*args, "--dry-run", check=False)
+    assert r.returncode != 0 and msg in (r.stderr + r.stdout)
+
+
+def test_default_output_name_and_positional_type(tmp_path):
+    src = tmp_path / "in.gguf"
+    small_model(src, odd=False)
+    r = run_cli(src, "Q4_K_M", "--dry-run")
+    assert f"-> {tmp_path / 'ggml-model-Q4_K_M.gguf'}" in r.stdout
+
+
+def test_fallback_to_a_type_without_kernel_is_an_error(tmp_path):
+    # IQ2_XXS on a 40-column tensor falls back to F16, which has no quantizer
+    src = tmp_path / "in.gguf"
+    small_model(src)
+    r = run_cli(src, tmp_path / "o.gguf", "iq2_xxs", "--dry-run", check=False)
+    assert r.returncode != 0 and "F16 for 1 tensors" in r.stderr
+
+
+def test_missing_kernel_type_is_an_error(tmp_path):
+    # Q4_0 with an imatrix asks for Q4_1 on the first ffn_down layers (no kernel)
+    src = tmp_path / "in.gguf"
+    io.write_gguf(src, "llama", [KV("llama.block_count", VT.UINT32, 8)],
+                  [(f"blk.{i}.ffn_down.weight", (256, 32), GT.F32,
+                    np.zeros((32, 256), np.float32)) for i in range(8)])
+    im = tmp_path / "im.gguf"
+    imatrix_for(im, {f"blk.{i}.ffn_down.weight": 256 for i in range(8)})
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--imatrix", im, "--dry-run", check=False)
+    assert r.returncode != 0 and "Q4_1" in r.stderr

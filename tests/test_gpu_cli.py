@@ -1,0 +1,85 @@
+"""GPU end-to-end: the command line quantizes synthetic GGUF files on the
+MI355X; every quantized tensor must equal the CPU oracle byte for byte, and
+the file must keep the reference's container contract (tests/test_q4_0.py:
+73-125): KVs preserved, file_type / quantization_version set, loader order,
+shapes, untouched passthroughs, output independent of --mem chunking."""
+
+from __future__ import annotations
+
+import importlib
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from cli_models import GT, imatrix_for, io, small_model
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parent.parent
+sch = importlib.import_module("quant-studio_amd.scheme")
+
+
+def run_cli(*args):
+    print("cli:", *args, flush=True)
+    r = subprocess.run([sys.executable, str(ROOT / "quant-studio.py"), *map(str, args)],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr + r.stdout
+    return r
+
+
+def check_output(src: Path, dst: Path, expect: dict, ftype: int, imatrix: dict | None = None):
+    r_in, r_out = io.GGUFReader(src), io.GGUFReader(dst)
+    kin, kout = r_in.values(), r_out.values()
+    for k, v in kin.items():
+        if k not in ("general.file_type",):
+            assert kout[k] == v, k
+    assert kout["general.file_type"] == ftype
+    assert kout["general.quantization_version"] == 2
+    assert [t.name for t in r_out.tensors] == sorted((t.name for t in r_in.tensors), key=sch.weight_name_key)
+    tin = {t.name: t for t in r_in.tensors}
+    for t in r_out.tensors:
+        s = tin[t.name]
+        assert t.ne == s.ne, t.name
+        if t.ggml_type == s.ggml_type:
+            assert np.array_equal(t.data, s.data), f"{t.name}: passthrough bytes changed"
+            continue
+        name = {v: k for k, v in oracle.TYPE_IDS.items()}[int(t.ggml_type)]
+        x = expect[t.name].reshape(-1, t.ne[0])
+        qw = None
+        if imatrix is not None and t.name in imatrix and name != "q4_0":
+            qw = imatrix[t.name][:t.ne[0]].astype(np.float32)
+        ref = oracle.quantize(name, x, qw)
+        assert np.array_equal(t.rows(), ref), f"{t.name} ({name}) differs from the oracle"
+    r_in.close()
+    r_out.close()
+
+
+def test_q4_0_small_model_multi_chunk(tmp_path):
+    src = tmp_path / "in.gguf"
+    expect = small_model(src)
+    a, b = tmp_path / "a.gguf", tmp_path / "b.gguf"
+    run_cli(src, a, "q4_0", "--mem", "64K")
+    run_cli(src, b, "q4_0")
+    assert a.read_bytes() == b.read_bytes()
+    check_output(src, a, expect, ftype=2)
+
+
+@pytest.mark.parametrize("scheme,ftype,extra", [
+    ("Q4_K_M", 15, []), ("Q6_K", 18, []), ("IQ4_XS", 30, []), ("Q2_K", 10, []),
+    ("IQ2_XXS", 19, ["--token-embedding-type", "q4_0"]),
+    ("IQ3_XXS", 23, []), ("IQ2_S", 28, []), ("IQ3_S", 26, []), ("Q3_K_L", 13, []),
+])
+def test_schemes_with_imatrix(tmp_path, scheme, ftype, extra):
+    src = tmp_path / "in.gguf"
+    expect = small_model(src, odd=False)
+    im = tmp_path / "im.gguf"
+    ks = {n: 256 for n in expect}
+    imatrix_for(im, ks, n_mat={"blk.0.ffn_gate_exps.weight": 4})
+    imat = io.load_imatrix(im)
+    out = tmp_path / "o.gguf"
+    run_cli(src, out, scheme, "--imatrix", im, "--mem", "128K", *extra)
+    check_output(src, out, expect, ftype=ftype, imatrix=imat)
