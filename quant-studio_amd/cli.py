@@ -220,7 +220,7 @@ def main(argv: list[str] | None = None) -> int:
     from .pipeline import HipPipeline, OrderedWriter, copy_tensor
     if not torch.cuda.is_available():
         sys.exit("error: no ROCm device available (this build has no CPU quantization path)")
-    device = torch.device("cuda" if args.device in ("auto", "cuda", "hip")
+    device = torch.device("cuda:0" if args.device in ("auto", "cuda", "hip")
                           else "cuda:" + args.device.split(":")[1])
     torch.cuda.set_device(device)
 
@@ -240,6 +240,9 @@ def main(argv: list[str] | None = None) -> int:
         if dst is not None:
             qw = None
             if spec.uses_imatrix and t.name in imatrix:
+                if imatrix[t.name].size < t.ne[0]:
+                    sys.exit(f"error: imatrix data for {t.name} has {imatrix[t.name].size} values, "
+                             f"rows have {t.ne[0]}")
                 qw = torch.from_numpy(imatrix[t.name][:t.ne[0]].copy()).to(device)
             rows_per_chunk = max(1, mem_bytes // (t.ne[0] * spec.bytes_per_elem))
             nbytes = pipe.quantize_tensor(t, int(dst), qw, rows_per_chunk, quantize)

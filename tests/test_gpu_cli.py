@@ -77,7 +77,7 @@ def test_schemes_with_imatrix(tmp_path, scheme, ftype, extra):
     src = tmp_path / "in.gguf"
     expect = small_model(src, odd=False)
     im = tmp_path / "im.gguf"
-    ks = {n: 256 for n in expect}
+    ks = {n: v.shape[-1] for n, v in expect.items()}
     imatrix_for(im, ks, n_mat={"blk.0.ffn_gate_exps.weight": 4})
     imat = io.load_imatrix(im)
     out = tmp_path / "o.gguf"
