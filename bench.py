@@ -157,6 +157,102 @@ def copy_peak(torch, dev, steps: int, warmup: int) -> int:
     return 0
 
 
+# ---------------------------------------------------------------------------
+# end-to-end: the CLI on a synthetic 4B-class bf16 GGUF
+# ---------------------------------------------------------------------------
+
+def synth_model(torch, dev, path: Path, im_path: Path, seed: int = 0) -> int:
+    """Qwen3-like 4B-class bf16 model: 36 layers, hidden 2560, ffn 9728, 32 q /
+    8 kv heads of dim 128, vocab 151936, tied embeddings; weights N(0, 0.02),
+    embedding N(0, 0.01). Imatrix per tensor: per-column log-normal(0, 1).
+    Values are drawn on the GPU; returns the number of weight values."""
+    import numpy as np
+    qs_io = importlib.import_module("quant-studio_amd.gguf_io")
+    GT = importlib.import_module("quant-studio_amd.gguf_types").GGMLQuantizationType
+    KV, VT = qs_io.KV, qs_io.VT
+    L, H, F, V = 36, 2560, 9728, 151936
+    tensors = [("token_embd.weight", (H, V), 0.01)]
+    for i in range(L):
+        p = f"blk.{i}."
+        tensors += [(p + "attn_norm.weight", (H,), None), (p + "attn_q.weight", (H, 4096), 0.02),
+                    (p + "attn_k.weight", (H, 1024), 0.02), (p + "attn_v.weight", (H, 1024), 0.02),
+                    (p + "attn_q_norm.weight", (128,), None), (p + "attn_k_norm.weight", (128,), None),
+                    (p + "attn_output.weight", (4096, H), 0.02), (p + "ffn_norm.weight", (H,), None),
+                    (p + "ffn_gate.weight", (H, F), 0.02), (p + "ffn_up.weight", (H, F), 0.02),
+                    (p + "ffn_down.weight", (F, H), 0.02)]
+    tensors.append(("output_norm.weight", (H,), None))
+    kvs = [KV("qwen3.block_count", VT.UINT32, L), KV("qwen3.context_length", VT.UINT32, 40960),
+           KV("qwen3.embedding_length", VT.UINT32, H), KV("qwen3.feed_forward_length", VT.UINT32, F),
+           KV("qwen3.attention.head_count", VT.UINT32, 32),
+           KV("qwen3.attention.head_count_kv", VT.UINT32, 8),
+           KV("qwen3.attention.key_length", VT.UINT32, 128),
+           KV("general.file_type", VT.UINT32, 32), KV("general.name", VT.STRING, "synthetic-4b")]
+    w = qs_io.GGUFWriter(path, "qwen3")
+    for kv in kvs:
+        w.add_kv(kv)
+    for name, ne, std in tensors:
+        n = int(np.prod(ne))
+        w.add_tensor_info(name, ne, GT.BF16 if std else GT.F32, n * (2 if std else 4))
+    f = w.write_header()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    n_weights = 0
+    im_tensors = []
+    for name, ne, std in tensors:
+        w.pad()
+        n = int(np.prod(ne))
+        if std is None:
+            f.write(np.ones(n, np.float32).tobytes())
+            continue
+        t = (torch.randn(n, device=dev, generator=g) * std).to(torch.bfloat16)
+        f.write(t.view(torch.int16).cpu().numpy().tobytes())
+        n_weights += n
+        v = rng.lognormal(0.0, 1.0, ne[0]).astype(np.float32)
+        im_tensors += [(name + ".in_sum2", (ne[0],), GT.F32, v * np.float32(100.0)),
+                       (name + ".counts", (1,), GT.F32, np.array([100.0], np.float32))]
+    w.pad()
+    w.close()
+    qs_io.write_gguf(im_path, "imatrix", [KV("general.type", VT.STRING, "imatrix")], im_tensors)
+    return n_weights
+
+
+def run_e2e(torch, dev, schemes: list[str]) -> int:
+    import re
+    import subprocess
+    import tempfile
+    base = Path("/dev/shm") if Path("/dev/shm").is_dir() else Path(tempfile.gettempdir())
+    with tempfile.TemporaryDirectory(dir=base) as d:
+        d = Path(d)
+        src, im = d / "model-bf16.gguf", d / "imatrix.gguf"
+        t0 = time.perf_counter()
+        n = synth_model(torch, dev, src, im)
+        gen_s = time.perf_counter() - t0
+        results = {}
+        for sch in schemes:
+            name, *extra = sch.split()
+            out = d / f"out-{name}.gguf"
+            cmd = [sys.executable, str(ROOT / "quant-studio.py"), str(src), str(out), name,
+                   "--imatrix", str(im), *extra]
+            t0 = time.perf_counter()
+            r = subprocess.run(cmd, capture_output=True, text=True)
+            wall = time.perf_counter() - t0
+            if r.returncode != 0:
+                print(r.stderr[-2000:], file=sys.stderr)
+                return 1
+            m = re.search(r"done in ([0-9.]+)s", r.stdout)
+            results[sch] = {"pipeline_s": float(m.group(1)) if m else None,
+                            "process_wall_s": round(wall, 2),
+                            "input_GBps_pipeline": round(src.stat().st_size / 1e9 / float(m.group(1)), 2)
+                            if m and float(m.group(1)) > 0 else None,
+                            "out_bytes": out.stat().st_size}
+            out.unlink()
+            print(f"e2e {sch}: {results[sch]}", file=sys.stderr, flush=True)
+        print(json.dumps({"e2e": "synthetic 4B-class bf16 GGUF (36 layers, 2560/9728, vocab 151936), "
+                                 "file in page cache", "file_bytes": src.stat().st_size,
+                          "weights": n, "generate_s": round(gen_s, 1), "runs": results}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +260,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--types", default="all", help="per-type table: all, none or a comma list")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--e2e", default=None,
+                    help="run the CLI end to end on a synthetic 4B-class model for these "
+                         "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M') and print its own JSON line")
     ap.add_argument("--copy-only", action="store_true",
                     help="time a plain 1 GiB device copy instead (HBM copy peak, and the "
                          "reference size for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counts)")
@@ -180,6 +279,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.copy_only:
         return copy_peak(torch, dev, args.steps, args.warmup)
+    if args.e2e:
+        return run_e2e(torch, dev, [x.strip() for x in args.e2e.split(";") if x.strip()])
     xs, qws, host = make_inputs(torch, dev)
     per_step_bytes = sum(2 * r * k for r, k in SHAPES)
     nrot = max(1, -(-ROTATE_BYTES // per_step_bytes))
