@@ -72,9 +72,11 @@ bool has_kernel(int id) { return find_type(id) != nullptr; }
 enum IqTabId { IQT_G2_256, IQT_G2_512, IQT_G2_1024, IQT_G3_256, IQT_G3_512, IQT_N };
 
 struct HostTab {
-    std::vector<uint16_t> grid, nlen, nbr;
-    std::vector<int16_t> kmap;
-    std::vector<int32_t> nstart;
+    std::vector<uint16_t> grid, nbr;
+    std::vector<uint32_t> cinfo;       // IQ2 layout described at qs::IqTabDev
+    std::vector<uint16_t> kmap16, lnbr;   // IQ3 layout described at qs::IqTabDev
+    int code0 = 0;
+    bool ok = true;
 };
 
 // kmap plus, for every off-grid code the level projection can produce (IQ2:
@@ -86,15 +88,18 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant) {
     const int ksize = bits == 2 ? 43692 : 4096;
     HostTab t;
     t.grid.assign(grid, grid + gs);
-    t.kmap.assign(ksize, -1);
-    t.nstart.assign(ksize, 0);
-    t.nlen.assign(ksize, 0);
-    for (int i = 0; i < gs; i++) t.kmap[grid[i]] = (int16_t)i;
+    t.cinfo.assign(ksize, 0);
+    std::vector<int> kmap(ksize, -1);
+    for (int i = 0; i < gs; i++) {
+        kmap[grid[i]] = i;
+        t.cinfo[grid[i]] = qs::CI_ON_GRID | (uint32_t)i;
+    }
+    t.code0 = kmap[0] >= 0 ? kmap[0] : 0;
     std::vector<int> gl(gs * nsub), d2(gs);
     for (int i = 0; i < gs; i++)
         for (int j = 0; j < nsub; j++) gl[i * nsub + j] = 2 * ((grid[i] >> (bits * j)) & lmask) + 1;
     for (int c = 0; c < ksize; c++) {
-        if (t.kmap[c] >= 0) continue;
+        if (kmap[c] >= 0) continue;
         int p[8];
         bool ok = true;
         for (int j = 0; j < nsub; j++) {
@@ -113,11 +118,29 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant) {
         std::sort(dist.begin(), dist.end());
         dist.erase(std::unique(dist.begin(), dist.end()), dist.end());
         const int limit = dist[std::min<int>(nwant, (int)dist.size()) - 1];
-        t.nstart[c] = (int32_t)t.nbr.size();
+        const size_t start = t.nbr.size();     // a multiple of 8: 16-byte aligned
         for (int rank = 0; rank < (int)dist.size() && dist[rank] <= limit; rank++)
             for (int i = 0; i < gs; i++)
                 if (d2[i] == dist[rank]) t.nbr.push_back((uint16_t)i);
-        t.nlen[c] = (uint16_t)(t.nbr.size() - t.nstart[c]);
+        const size_t len = t.nbr.size() - start;
+        t.nbr.resize((t.nbr.size() + 7) / 8 * 8, 0);
+        t.cinfo[c] = (uint32_t)((start / 8) << 12) | (uint32_t)len;
+        t.ok = t.ok && len < 4096 && start / 8 < (1u << 19);
+    }
+    if (bits == 3) {
+        // 16-bit map and length-prefixed lists; positions must fit in 15 bits
+        t.kmap16.assign(ksize, 0);
+        for (int c = 0; c < ksize; c++) {
+            if (t.cinfo[c] & qs::CI_ON_GRID) {
+                t.kmap16[c] = (uint16_t)(qs::K16_ON_GRID | (t.cinfo[c] & 0xffffu));
+                continue;
+            }
+            const size_t pos = t.lnbr.size(), len = t.cinfo[c] & 0xfffu, st = 8 * (size_t)(t.cinfo[c] >> 12);
+            t.ok = t.ok && pos < qs::K16_ON_GRID;
+            t.kmap16[c] = (uint16_t)pos;
+            t.lnbr.push_back((uint16_t)len);
+            t.lnbr.insert(t.lnbr.end(), t.nbr.begin() + st, t.nbr.begin() + st + len);
+        }
     }
     return t;
 }
@@ -160,11 +183,12 @@ bool device_tabs(std::array<qs::IqTabDev, IQT_N>& out) {
         for (int id = 0; id < IQT_N; id++) {
             const HostTab& h = host_tab(id);
             d[id].grid = upload(h.grid);
-            d[id].kmap = upload(h.kmap);
-            d[id].nstart = upload(h.nstart);
-            d[id].nlen = upload(h.nlen);
+            d[id].cinfo = upload(h.cinfo);
             d[id].nbr = upload(h.nbr);
-            if (!d[id].grid || !d[id].kmap || !d[id].nstart || !d[id].nlen || !d[id].nbr) return false;
+            d[id].kmap16 = upload(h.kmap16);
+            d[id].lnbr = upload(h.lnbr);
+            d[id].code0 = h.code0;
+            if (!h.ok || !d[id].grid || !d[id].cinfo || !d[id].nbr || !d[id].kmap16 || !d[id].lnbr) return false;
         }
         it = g_dev_tabs.emplace(dev, d).first;
     }

@@ -18,13 +18,42 @@
 namespace qs {
 
 // Device copy of one grid's tables (built once per device on the host).
+// IQ2 grids: cinfo packs everything a projection needs about a code:
+//   on-grid:  bit 31 set, bits 0..15 = grid index;
+//   off-grid: bits 12..30 = first neighbour / 8, bits 0..11 = list length;
+// each list starts on a 16-byte boundary of nbr, so a lane fetches eight
+// candidates with one vector load.
+// IQ3 grids (4096 codes, short lists): kmap16 fits in LDS at 2 bytes a code,
+//   on-grid:  bit 15 set, bits 0..14 = grid index;
+//   off-grid: position of the code's list in lnbr, stored as [len, i0, i1 ...].
 struct IqTabDev {
     const uint16_t* grid;     // grid codes (BITS-bit levels per value)
-    const int16_t* kmap;      // code -> grid index, -1 when off-grid
-    const int32_t* nstart;    // code -> first neighbour in nbr
-    const uint16_t* nlen;     // code -> neighbour count (off-grid codes)
-    const uint16_t* nbr;      // neighbour grid indices, (distance, index) order
+    const uint32_t* cinfo;    // IQ2: code -> packed kmap / list position / length
+    const uint16_t* nbr;      // IQ2: neighbour grid indices, (distance, index) order
+    const uint16_t* kmap16;   // IQ3: code -> grid index | list position
+    const uint16_t* lnbr;     // IQ3: length-prefixed neighbour lists
+    int code0;                // grid index of the all-zero code (0 if off-grid)
 };
+
+constexpr uint32_t CI_ON_GRID = 0x80000000u;
+constexpr uint32_t K16_ON_GRID = 0x8000u;
+
+// LDS of the IQ kernels: x^2 staging for the superblock sum, per-group
+// scales, and the packed output blocks.
+template <int SPW, int BYTES>
+struct alignas(16) IqLds {
+    float v[SPW][QK_K];
+    float tmp[SPW][40];
+    float sc[SPW][16];
+    uint8_t out[SPW * BYTES + 16];
+};
+
+template <int SPW, int BYTES>
+QS_DEV void sb_store(const IqLds<SPW, BYTES>& s, const KArgs& a) {
+    const int64_t first = (int64_t)blockIdx.x * SPW;
+    const int64_t nvalid = min((int64_t)SPW, a.n_units - first);
+    store_staged(s.out, a.dst, first * BYTES, (int)nvalid * BYTES);
+}
 
 template <int I, int END, typename F>
 QS_DEV void static_for(F&& f) {
@@ -46,7 +75,7 @@ QS_DEV float grid_value(uint32_t gcode, int j) {
 // IQ2 distances are a left-to-right sum of 8 terms from +0; IQ3's are
 // ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and diff = sc*g - x.
 template <int BITS, int NV, int OFF, int N>
-QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const int16_t* kmap_lds,
+QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const uint16_t* kmap_lds,
                       const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool& on) {
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
     int code = 0;
@@ -57,27 +86,66 @@ QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const int16_t* km
         t = 0.5f * t;
         code |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
     }
-    const int g = kmap_lds ? (int)kmap_lds[code] : (int)T.kmap[code];
-    on = g >= 0;
-    if (g >= 0) return g;
-    const int st = T.nstart[code], n = T.nlen[code];
     float best = __builtin_inff();
     int bi = -1;
-    for (int k = 0; k < n; k++) {
-        const int gi = T.nbr[st + k];
-        const uint32_t gc = glds[gi];
-        float d2 = 0.0f;
+    if constexpr (BITS == 3) {
+        // short lists (about five entries): one candidate per iteration, the
+        // next index loaded while this one is evaluated
+        const uint32_t k16 = kmap_lds[code];
+        on = (k16 & K16_ON_GRID) != 0;
+        if (on) return (int)(k16 & 0x7fffu);
+        const uint16_t* lp = T.lnbr + k16;
+        const int n = lp[0];
+        int gi = lp[1];
+        for (int k = 0; k < n; k++) {
+            const int nxt = (k + 1 < n) ? (int)lp[k + 2] : 0;
+            const uint32_t gc = glds[gi];
+            float d2 = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NV; j++) {
-            float diff = sc * grid_value<BITS>(gc, j);
-            diff = diff - xv[OFF + j];
-            const float t = (wv[OFF + j] * diff) * diff;
-            if constexpr (NV == 4) d2 = (j == 0) ? t : d2 + t;
-            else d2 = d2 + t;
+            for (int e = 0; e < NV; e++) {
+                float diff = sc * grid_value<BITS>(gc, e);
+                diff = diff - xv[OFF + e];
+                const float t = (wv[OFF + e] * diff) * diff;
+                d2 = (e == 0) ? t : d2 + t;
+            }
+            if (d2 < best) {
+                best = d2;
+                bi = gi;
+            }
+            gi = nxt;
         }
-        if (d2 < best) {
-            best = d2;
-            bi = gi;
+    } else {
+        // IQ2 lists are long (tens of entries): eight indices per 16-byte load,
+        // the next eight in flight while these are evaluated
+        const uint32_t ci = T.cinfo[code];
+        on = (ci & CI_ON_GRID) != 0;
+        if (on) return (int)(ci & 0xffffu);
+        const int n = (int)(ci & 0xfffu);
+        const uint4* lp = reinterpret_cast<const uint4*>(T.nbr) + ((ci >> 12) & 0x7ffffu);
+        uint4 nxt = lp[0];
+        for (int k = 0; k < n; k += 8) {
+            const uint4 c = nxt;
+            if (k + 8 < n) nxt = lp[(k >> 3) + 1];
+            const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (k + j < n) {
+                    const int gi = (int)((w4[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    const uint32_t gc = glds[gi];
+                    float d2 = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < NV; e++) {
+                        float diff = sc * grid_value<BITS>(gc, e);
+                        diff = diff - xv[OFF + e];
+                        const float t = (wv[OFF + e] * diff) * diff;
+                        d2 = d2 + t;
+                    }
+                    if (d2 < best) {
+                        best = d2;
+                        bi = gi;
+                    }
+                }
+            }
         }
     }
     return bi;
@@ -139,6 +207,37 @@ QS_DEV void iq_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w
     }
 }
 
+// the same two sums reduced as tree_sum over the whole group: NV is a power
+// of two, so the group's pairwise tree is each subgroup's own tree followed by
+// a tree over the NSUB subgroup sums; reducing per subgroup keeps 2*NSUB
+// partials live instead of 2*N products
+template <int BITS, int NV, int NSUB, int N>
+QS_DEV void iq_tree_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
+                         float& sumqx, float& sumq2) {
+    static_assert(NV * NSUB == N && (NV & (NV - 1)) == 0, "subgroups must tile the group");
+    float sa[NSUB], sb[NSUB];
+#pragma unroll
+    for (int s = 0; s < NSUB; s++) {
+        const uint32_t gc = glds[gi[s]];
+        float a[NV], b[NV];
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            const float q = grid_value<BITS>(gc, j);
+            a[j] = (w[NV * s + j] * xval[NV * s + j]) * q;
+            b[j] = (w[NV * s + j] * q) * q;
+        }
+        sa[s] = tree_sum(a);
+        sb[s] = tree_sum(b);
+    }
+    if constexpr (NSUB == 1) {
+        sumqx = sa[0];
+        sumq2 = sb[0];
+    } else {
+        sumqx = tree_sum(sa);
+        sumq2 = tree_sum(sb);
+    }
+}
+
 // superblock scale nibbles: d = max/31, l = clamp(round(0.5*(sc/d - 1)), 0, 15)
 // (iq2.py:92-96, iq2xs_common.py:345-355, iq3_xxs.py:115-121)
 template <int NG>
@@ -190,7 +289,7 @@ QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float* vlds, float* 
 template <int SRC>
 __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4, IqSteps sweep) {
     constexpr int LPS = 8, SPW = 8, BYTES = 66;
-    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[256];
     for (int i = threadIdx.x; i < 256; i += 64) glds[i] = T.grid[i];
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
@@ -211,7 +310,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
     active = active && eff > 0;
     const float eff_safe = active ? eff : 1.0f;
     float scale = scale0, best = 0.0f;
-    const int zero_gi = T.kmap[0] >= 0 ? T.kmap[0] : 0;
+    const int zero_gi = T.code0;
     int L[4] = {zero_gi, zero_gi, zero_gi, zero_gi};
     float ta[32], tb[32];
 #pragma unroll 1
@@ -286,7 +385,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
 template <int SRC, bool IS_S>
 __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
     constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 82 : 74, GS = IS_S ? 1024 : 512;
-    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[GS];
     __shared__ int wlds[SPW][16][2];
     for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
@@ -309,11 +408,10 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
     for (int i = 1; i < 16; i++) gmax = fmaxf(gmax, xval[i]);
     const bool active = IS_S ? gmax >= 1e-8f : gmax >= GROUP_MAX_EPS;
     const float gsafe = active ? gmax : 1.0f;
-    const int code0 = T.kmap[0] >= 0 ? T.kmap[0] : 0;
+    const int code0 = T.code0;
     float scale = active ? gmax / 5.0f : 0.0f, best = 0.0f;
     int win[2] = {code0, code0};
     bool og[2] = {true, true};
-    float ta[16], tb[16];
 #pragma unroll 1
     for (int st = 0; st < sweep.n; st++) {
         const float inv = rdiv(sweep.v[st], gsafe), sc = 1.0f / inv;
@@ -321,8 +419,8 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         bool on[2];
         gi[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, sc, on[0]);
         gi[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, sc, on[1]);
-        iq_sums<2, 8, 2>(glds, gi, w, xval, ta, tb);
-        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        float sumqx, sumq2;
+        iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             const float ns = sumqx / fmaxf(sumq2, F32_TINY);
             scale = ns;
@@ -339,8 +437,8 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         bool on;
         if (!og[0]) win[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, scale, on);
         if (!og[1]) win[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, scale, on);
-        iq_sums<2, 8, 2>(glds, win, w, xval, ta, tb);
-        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        float sumqx, sumq2;
+        iq_tree_sums<2, 8, 2>(glds, win, w, xval, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
     }
     if (active && scale < 0) {
@@ -401,14 +499,14 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
 // iq3_s.py:31-140
 // ------------------------------------------------------------------
 template <int SRC, bool IS_S, bool IMAT>
-__global__ __launch_bounds__(64) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
     constexpr int LPS = 8, SPW = 8, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
-    __shared__ SbLds<SPW, BYTES> s;
+    __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[GS];
-    __shared__ int16_t klds[4096];
+    __shared__ uint16_t klds[4096];
     __shared__ int act_lds[SPW][8];
     for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
-    for (int i = threadIdx.x; i < 4096; i += 64) klds[i] = T.kmap[i];
+    for (int i = threadIdx.x; i < 4096; i += 64) klds[i] = T.kmap16[i];
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
@@ -434,7 +532,6 @@ __global__ __launch_bounds__(64) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) 
         Wg[k] = 0;
         og[k] = !IS_S;
     }
-    float ta[32], tb[32];
     wave_sync();   // glds / klds ready
 #pragma unroll 1
     for (int st = 0; st < steps.n; st++) {
@@ -442,8 +539,8 @@ __global__ __launch_bounds__(64) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) 
         int gi[8];
         bool on[8];
         static_for<0, 8>([&](auto S) { gi[S] = iq_project<3, 4, 4 * S>(T, glds, klds, xval, waux, inv, sc, on[S]); });
-        iq_sums<3, 4, 8>(glds, gi, w, xval, ta, tb);
-        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        float sumqx, sumq2;
+        iq_tree_sums<3, 4, 8>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             const float ns = sumqx / fmaxf(sumq2, F32_TINY);
             scale = ns;
@@ -467,8 +564,8 @@ __global__ __launch_bounds__(64) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) 
 #pragma unroll
         for (int k = 0; k < 8; k++)
             if (redo && (IS_S || !og[k])) Wg[k] = w2[k];
-        iq_sums<3, 4, 8>(glds, Wg, w, xval, ta, tb);
-        const float sumqx = tree_sum(ta), sumq2 = tree_sum(tb);
+        float sumqx, sumq2;
+        iq_tree_sums<3, 4, 8>(glds, Wg, w, xval, sumqx, sumq2);
         if (redo && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
     }
     if (active && scale < 0) {
