@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QS_ABI_VERSION 1
+#define QS_ABI_VERSION 2
 
 #define QS_EINVAL (-22)
 #define QS_ENOTSUP (-95)
@@ -89,6 +89,51 @@ int qs_quantize(int ggml_type, int src_type, const void *src, int64_t n_rows, in
 
 /* Message describing the last failure on the calling thread ("" if none). */
 const char *qs_last_error(void);
+
+/* ---- host pipeline of the command line ----
+ *
+ * Replaces the reference's CudaPipeline (quant-studio.py:148-213), its
+ * OutputWriter (:103-131) and copy_tensor (:235-241): rows are read from host
+ * memory (normally the input file's mapping) chunk by chunk, staged through
+ * pinned buffers, quantized on the device and written with pwrite() at the
+ * tensor's offset in the output file. The caller keeps the GGUF header,
+ * tensor order and offsets, the type plan and the chunk size (--mem).
+ * All calls on one pipeline come from one thread. Host memory passed in must
+ * stay valid, and fd open, until qs_pipeline_finish() returns.
+ */
+typedef struct qs_pipeline qs_pipeline;
+
+/* Number of visible ROCm devices (0 when there are none or HIP fails). The
+ * reference's device choice tests torch.cuda.is_available() (pick_device,
+ * quant-studio.py:51-58). */
+int qs_device_count(void);
+
+/* Pipeline on `device` with n_slots chunk slots (2..16; 3 keeps host copy,
+ * H2D, kernel and D2H+write of consecutive chunks overlapped) and
+ * n_copy_threads host threads (1..64) for the mapping -> pinned copies. */
+int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline **out);
+
+/* Queue one tensor: n_rows rows of k values of src_type at host address src
+ * (rows contiguous), quantized to ggml_type in chunks of rows_per_chunk rows
+ * with the host imatrix (k floats or NULL; as qs_quantize), the output rows
+ * written contiguously at out_offset of fd. Returns once every chunk is
+ * queued; blocks only while all slots are busy. One pipeline.quantize_tensor
+ * call of the reference (quant-studio.py:180-213, driven from :453-461). */
+int qs_pipeline_quantize(qs_pipeline *p, int ggml_type, int src_type, const void *src,
+                         int64_t n_rows, int64_t k, const float *imatrix,
+                         int64_t rows_per_chunk, int fd, int64_t out_offset);
+
+/* Queue a write of nbytes host bytes at out_offset of fd, in order with the
+ * quantized chunks (a passthrough tensor, copy_tensor quant-studio.py:235-241). */
+int qs_pipeline_write(qs_pipeline *p, const void *src, int64_t nbytes, int fd, int64_t out_offset);
+
+/* Wait until everything queued is written (OutputWriter.flush,
+ * quant-studio.py:128-130); returns the first failure of any queued step. */
+int qs_pipeline_finish(qs_pipeline *p);
+
+/* Wait for queued work, then release the pipeline's threads, buffers,
+ * streams and events. NULL is ignored. */
+void qs_pipeline_destroy(qs_pipeline *p);
 
 #ifdef __cplusplus
 }

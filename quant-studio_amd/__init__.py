@@ -6,7 +6,8 @@ kernels/common.py:20-37): `QUANT_TYPES` maps a lowercase type name to a
 Here every quant_fn is one call into the gfx950 HIP library (libqs_hip.so,
 C ABI in include/quant_studio.h) on torch's current stream. There is no CPU
 path: the library must be built (build.py) and a ROCm device present, and
-every failure raises.
+every failure raises. torch is imported on first use of the tensor API only;
+the command line runs on the library's own pipeline without it.
 
 Import with `importlib.import_module("quant-studio_amd")` (the directory name
 is not an identifier).
@@ -18,24 +19,33 @@ import ctypes
 import sys
 from pathlib import Path
 
-import torch
-
 from .gguf_types import GGMLQuantizationType, LlamaFileType
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "_build" / "libqs_hip.so"
-
-F32_TINY = torch.finfo(torch.float32).tiny
-
-# source dtypes the quantizers read directly (kernels/common.py:20-24)
-TORCH_DTYPES = {
-    GGMLQuantizationType.F32: torch.float32,
-    GGMLQuantizationType.F16: torch.float16,
-    GGMLQuantizationType.BF16: torch.bfloat16,
-}
-_SRC_IDS = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 30}
+ABI_VERSION = 2
 
 _lib: ctypes.CDLL | None = None
+
+
+def __getattr__(name: str):
+    # torch-valued constants, created when first asked for
+    if name in ("TORCH_DTYPES", "F32_TINY"):
+        import torch
+        # source dtypes the quantizers read directly (kernels/common.py:20-24)
+        globals()["TORCH_DTYPES"] = {
+            GGMLQuantizationType.F32: torch.float32,
+            GGMLQuantizationType.F16: torch.float16,
+            GGMLQuantizationType.BF16: torch.bfloat16,
+        }
+        globals()["F32_TINY"] = torch.finfo(torch.float32).tiny
+        return globals()[name]
+    raise AttributeError(name)
+
+
+def _src_id(dtype) -> int | None:
+    import torch
+    return {torch.float32: 0, torch.float16: 1, torch.bfloat16: 30}.get(dtype)
 
 
 class QuantSpecError(RuntimeError):
@@ -64,8 +74,23 @@ def library() -> ctypes.CDLL:
                                   ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                   ctypes.c_int64, ctypes.c_void_p]
         L.qs_last_error.restype = ctypes.c_char_p
-        if L.qs_abi_version() != 1:
-            raise ImportError(f"{LIB_PATH}: ABI version {L.qs_abi_version()} != 1")
+        L.qs_device_count.restype = ctypes.c_int
+        L.qs_pipeline_create.restype = ctypes.c_int
+        L.qs_pipeline_create.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.POINTER(ctypes.c_void_p)]
+        L.qs_pipeline_quantize.restype = ctypes.c_int
+        L.qs_pipeline_quantize.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int64, ctypes.c_int, ctypes.c_int64]
+        L.qs_pipeline_write.restype = ctypes.c_int
+        L.qs_pipeline_write.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                        ctypes.c_int64]
+        L.qs_pipeline_finish.restype = ctypes.c_int
+        L.qs_pipeline_finish.argtypes = [ctypes.c_void_p]
+        L.qs_pipeline_destroy.restype = None
+        L.qs_pipeline_destroy.argtypes = [ctypes.c_void_p]
+        if L.qs_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH}: ABI version {L.qs_abi_version()} != {ABI_VERSION}")
         _lib = L
     return _lib
 
@@ -81,18 +106,19 @@ def row_bytes(ggml_type: int, k: int) -> int:
     return rb
 
 
-def quantize(ggml_type: int, x: torch.Tensor, qw: torch.Tensor | None,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+def quantize(ggml_type: int, x, qw, out=None):
     """Quantize the rows of x (n, k) on its ROCm device; returns uint8 (n, row_bytes).
 
     x: float32 / float16 / bfloat16, unit stride along k, 16-byte aligned rows.
     qw: (k,) float32 imatrix column weights on the same device, or None.
     The launch goes on torch's current stream; nothing is synchronised."""
+    import torch
     if x.device.type != "cuda":
         raise ValueError(f"quant_fn: x must be on a ROCm device, got {x.device}")
     if x.dim() != 2:
         raise ValueError(f"quant_fn: x must be 2-D (n, k), got shape {tuple(x.shape)}")
-    if x.dtype not in _SRC_IDS:
+    src_id = _src_id(x.dtype)
+    if src_id is None:
         raise ValueError(f"quant_fn: unsupported dtype {x.dtype}")
     n, k = x.shape
     if x.stride(1) != 1 and k > 1:
@@ -110,7 +136,7 @@ def quantize(ggml_type: int, x: torch.Tensor, qw: torch.Tensor | None,
         qptr = qw.data_ptr()
     stride_bytes = (x.stride(0) if n > 1 else k) * x.element_size()
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = library().qs_quantize(int(ggml_type), _SRC_IDS[x.dtype], x.data_ptr(), n, k,
+    rc = library().qs_quantize(int(ggml_type), src_id, x.data_ptr(), n, k,
                                stride_bytes, qptr, out.data_ptr(), out.numel(), stream)
     if rc != 0:
         raise QuantSpecError(last_error())
@@ -132,7 +158,8 @@ class QuantSpec:
 
 
 def _kernel_factory(ggml_type: GGMLQuantizationType, uses_imatrix: bool):
-    def make_kernel(device: torch.device, qw):
+    def make_kernel(device, qw):
+        import torch
         q = qw if uses_imatrix else None    # Q4_0 ignores an imatrix (q4_0.py:36-37)
         if q is not None:
             q = q.to(device=device, dtype=torch.float32).contiguous()

@@ -27,7 +27,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
-SOURCES = ["qs_api.hip"]
+SOURCES = ["qs_api.hip", "qs_pipeline.cpp"]
 
 
 def build(verbose: bool = False) -> Path:

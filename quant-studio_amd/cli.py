@@ -12,6 +12,7 @@ on a ROCm device (`--device auto|cuda|hip`); there is no CPU path.
 from __future__ import annotations
 
 import argparse
+import os
 import sys
 import time
 from pathlib import Path
@@ -215,14 +216,20 @@ def main(argv: list[str] | None = None) -> int:
               f"({total_out / max(total_in, 1) * 100:.1f}%)")
         return 0
 
-    import torch
-    from . import quantize
-    from .pipeline import HipPipeline, OrderedWriter, copy_tensor
-    if not torch.cuda.is_available():
+    from . import row_bytes
+    from .pipeline import NativePipeline, PipelineError, device_count
+    ndev = device_count()
+    if ndev == 0:
         sys.exit("error: no ROCm device available (this build has no CPU quantization path)")
-    device = torch.device("cuda:0" if args.device in ("auto", "cuda", "hip")
-                          else "cuda:" + args.device.split(":")[1])
-    torch.cuda.set_device(device)
+    dev_index = 0 if args.device in ("auto", "cuda", "hip") else int(args.device.split(":")[1])
+    if dev_index >= ndev:
+        sys.exit(f"error: device {args.device!r} not present ({ndev} ROCm devices)")
+
+    # imatrix rows are checked before anything is written
+    for t, dst, spec in plans:
+        if dst is not None and spec.uses_imatrix and t.name in imatrix and imatrix[t.name].size < t.ne[0]:
+            sys.exit(f"error: imatrix data for {t.name} has {imatrix[t.name].size} values, "
+                     f"rows have {t.ne[0]}")
 
     writer = GGUFWriter(out_path, arch)
     for k in copied_kvs(reader, opt.ftype):
@@ -230,33 +237,35 @@ def main(argv: list[str] | None = None) -> int:
     for t, dst, _ in plans:
         writer.add_tensor_info(t.name, t.ne, dst if dst is not None else t.ggml_type, out_nbytes(t, dst))
     writer.write_header()
-    out = OrderedWriter(writer)
-    pipe = HipPipeline(device, out)
+    data_start = writer.data_start()
+    writer.fout.flush()
+    fd = writer.fout.fileno()
 
     total_in = total_out = 0
     t0 = time.time()
-    for i, (t, dst, spec) in enumerate(plans):
-        out.pad()
-        if dst is not None:
-            qw = None
-            if spec.uses_imatrix and t.name in imatrix:
-                if imatrix[t.name].size < t.ne[0]:
-                    sys.exit(f"error: imatrix data for {t.name} has {imatrix[t.name].size} values, "
-                             f"rows have {t.ne[0]}")
-                qw = torch.from_numpy(imatrix[t.name][:t.ne[0]].copy()).to(device)
-            rows_per_chunk = max(1, mem_bytes // (t.ne[0] * spec.bytes_per_elem))
-            nbytes = pipe.quantize_tensor(t, int(dst), qw, rows_per_chunk, quantize)
-        else:
-            nbytes = copy_tensor(t, mem_bytes, out)
-        total_in += t.nbytes
-        total_out += nbytes
-        shape = "x".join(str(d) for d in t.ne)
-        src = t.ggml_type.name
-        print(f"[{i + 1:4d}/{len(plans)}] {t.name:48s} {shape:>16s}  {src:>5s} -> "
-              f"{dst.name if dst else src:<8s} {fmt_size(t.nbytes)} -> {fmt_size(nbytes)}")
-    out.pad()
-    out.close()
-    pipe.close()
+    try:
+        with NativePipeline(dev_index, fd) as pipe:
+            for i, ((t, dst, spec), info) in enumerate(zip(plans, writer.infos)):
+                off = data_start + info[3]
+                if dst is not None:
+                    qw = imatrix.get(t.name) if spec.uses_imatrix else None
+                    rows_per_chunk = max(1, mem_bytes // (t.ne[0] * spec.bytes_per_elem))
+                    nbytes = pipe.quantize_tensor(t, int(dst), qw, rows_per_chunk, off,
+                                                  row_bytes(int(dst), t.ne[0]))
+                else:
+                    nbytes = pipe.write(t.data, off)
+                total_in += t.nbytes
+                total_out += nbytes
+                shape = "x".join(str(d) for d in t.ne)
+                src = t.ggml_type.name
+                print(f"[{i + 1:4d}/{len(plans)}] {t.name:48s} {shape:>16s}  {src:>5s} -> "
+                      f"{dst.name if dst else src:<8s} {fmt_size(t.nbytes)} -> {fmt_size(nbytes)}")
+            pipe.finish()
+    except PipelineError as e:
+        writer.close()
+        sys.exit(f"error: {e}")
+    # the padding after each tensor and at the end is zeros: set the final size
+    os.ftruncate(fd, writer.total_size())
     writer.close()
     dt = time.time() - t0
     print(f"done in {dt:.1f}s: {fmt_size(total_in)} -> {fmt_size(total_out)} "

@@ -15,14 +15,16 @@
 
 #include "quant_studio.h"
 #include "qs_grids.h"
+#include "qs_host.h"
 #include "qs_iq.h"
 #include "qs_kernels.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+namespace qs_host {
+
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -32,6 +34,14 @@ int fail(int code, const char* fmt, ...) {
     g_err = buf;
     return code;
 }
+
+void clear_error() { g_err.clear(); }
+
+}  // namespace qs_host
+
+namespace {
+
+using qs_host::fail;
 
 struct TypeInfo {
     int id;

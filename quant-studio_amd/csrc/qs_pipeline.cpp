@@ -1,0 +1,423 @@
+// Host pipeline of the command line: mapped GGUF rows -> pinned staging ->
+// HBM -> quantizer -> pinned -> pwrite at the tensor's file offset.
+//
+// Replaces the reference's CudaPipeline (quant-studio.py:148-213),
+// OutputWriter (:103-131) and copy_tensor (:235-241):
+//   - a ring of slots (pinned in/out, device in/out/imatrix), so the host copy
+//     of chunk i+2, the H2D of chunk i+1, the kernel of chunk i and the D2H
+//     and file write of chunk i-1 overlap;
+//   - the mapping -> pinned copy of a chunk split over a pool of threads (one
+//     thread caps the pipeline well below the PCIe rate);
+//   - H2D and D2H on a copy stream, kernels on a compute stream, ordered by
+//     events; the calling thread never waits on the GPU except for a slot;
+//   - rows handed to the kernel in their stored type (no f32 upcast pass);
+//   - one writer thread that waits on each chunk's D2H event and writes the
+//     chunk at its own offset, so the output never depends on the chunking.
+#include <hip/hip_runtime.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <cerrno>
+#include <condition_variable>
+#include <cstring>
+#include <deque>
+#include <functional>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "quant_studio.h"
+#include "qs_host.h"
+
+using qs_host::fail;
+
+namespace {
+
+constexpr size_t kCopyPart = size_t(4) << 20;     // smallest share of a chunk copy per thread
+
+// Fixed pool running the parts of one chunk copy; run() returns when all are done.
+class CopyPool {
+public:
+    explicit CopyPool(int n) {
+        for (int i = 0; i < n; i++) threads_.emplace_back([this] { loop(); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        for (auto& t : threads_) t.join();
+    }
+    int size() const { return (int)threads_.size(); }
+
+    void run(std::vector<std::function<void()>>& tasks) {
+        if (tasks.size() == 1 || threads_.empty()) {
+            for (auto& t : tasks) t();
+            return;
+        }
+        std::unique_lock<std::mutex> l(m_);
+        for (auto& t : tasks) q_.push_back(std::move(t));
+        pending_ += tasks.size();
+        cv_.notify_all();
+        done_cv_.wait(l, [this] { return pending_ == 0; });
+    }
+
+private:
+    void loop() {
+        std::unique_lock<std::mutex> l(m_);
+        for (;;) {
+            cv_.wait(l, [this] { return stop_ || !q_.empty(); });
+            if (q_.empty()) return;
+            auto t = std::move(q_.front());
+            q_.pop_front();
+            l.unlock();
+            t();
+            l.lock();
+            if (--pending_ == 0) done_cv_.notify_all();
+        }
+    }
+    std::vector<std::thread> threads_;
+    std::deque<std::function<void()>> q_;
+    std::mutex m_;
+    std::condition_variable cv_, done_cv_;
+    size_t pending_ = 0;
+    bool stop_ = false;
+};
+
+struct WriteJob {
+    hipEvent_t ev;            // wait for this before reading buf (nullptr: host data)
+    const void* buf;
+    size_t n;
+    int fd;
+    int64_t off;
+};
+
+// Single writer thread: jobs complete in submission order; done() counts them.
+class Writer {
+public:
+    explicit Writer(int device) : th_([this, device] { (void)hipSetDevice(device); loop(); }) {}
+    ~Writer() {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            stop_ = true;
+        }
+        cv_.notify_all();
+        th_.join();
+    }
+    uint64_t push(const WriteJob& j) {
+        std::lock_guard<std::mutex> l(m_);
+        q_.push_back(j);
+        cv_.notify_all();
+        return ++pushed_;
+    }
+    void wait(uint64_t seq) {
+        std::unique_lock<std::mutex> l(m_);
+        done_cv_.wait(l, [&] { return done_ >= seq; });
+    }
+    void drain() { wait(pushed()); }
+    uint64_t pushed() {
+        std::lock_guard<std::mutex> l(m_);
+        return pushed_;
+    }
+    // first error seen by the writer ("" if none)
+    std::string error() {
+        std::lock_guard<std::mutex> l(m_);
+        return err_;
+    }
+
+private:
+    void loop() {
+        std::unique_lock<std::mutex> l(m_);
+        for (;;) {
+            cv_.wait(l, [this] { return stop_ || !q_.empty(); });
+            if (q_.empty()) return;
+            WriteJob j = q_.front();
+            q_.pop_front();
+            const bool failed = !err_.empty();
+            l.unlock();
+            std::string e;
+            if (!failed) e = run(j);
+            l.lock();
+            if (!e.empty() && err_.empty()) err_ = e;
+            done_++;
+            done_cv_.notify_all();
+        }
+    }
+    static std::string run(const WriteJob& j) {
+        if (j.ev) {
+            const hipError_t he = hipEventSynchronize(j.ev);
+            if (he != hipSuccess) return std::string("device work failed: ") + hipGetErrorString(he);
+        }
+        const char* p = static_cast<const char*>(j.buf);
+        size_t left = j.n;
+        int64_t off = j.off;
+        while (left) {
+            const ssize_t w = pwrite(j.fd, p, std::min(left, size_t(1) << 30), off);
+            if (w < 0 && errno == EINTR) continue;
+            if (w <= 0) return std::string("write failed: ") + std::strerror(w < 0 ? errno : EIO);
+            p += w;
+            off += w;
+            left -= (size_t)w;
+        }
+        return "";
+    }
+    std::deque<WriteJob> q_;
+    std::mutex m_;
+    std::condition_variable cv_, done_cv_;
+    uint64_t pushed_ = 0, done_ = 0;
+    std::string err_;
+    bool stop_ = false;
+    std::thread th_;
+};
+
+struct PinnedBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    bool grow(size_t want) {
+        if (n >= want) return true;
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+        if (hipHostMalloc(&p, std::max<size_t>(want, 1), hipHostMallocDefault) != hipSuccess) return false;
+        n = want;
+        return true;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+    bool grow(size_t want) {
+        if (n >= want) return true;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+        if (hipMalloc(&p, std::max<size_t>(want, 1)) != hipSuccess) return false;
+        n = want;
+        return true;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+};
+
+struct Slot {
+    PinnedBuf in_pin, out_pin, qw_pin;
+    DevBuf x_dev, out_dev, qw_dev;
+    hipEvent_t h2d = nullptr, kern = nullptr, d2h = nullptr;
+    bool used = false;        // events recorded at least once
+    uint64_t write_seq = 0;   // writer job that reads out_pin
+};
+
+int elem_size(int src_type) {
+    switch (src_type) {
+    case QS_SRC_F32: return 4;
+    case QS_SRC_F16:
+    case QS_SRC_BF16: return 2;
+    default: return 0;
+    }
+}
+
+}  // namespace
+
+struct qs_pipeline {
+    int device = 0;
+    hipStream_t copy = nullptr, compute = nullptr;
+    std::vector<Slot> slots;
+    size_t next = 0;
+    std::unique_ptr<CopyPool> pool;
+    std::unique_ptr<Writer> writer;
+    std::string err;          // first failure; every later call reports it
+
+    int check_writer() {
+        if (err.empty()) err = writer->error();
+        return err.empty() ? 0 : fail(QS_EIO, "%s", err.c_str());
+    }
+    int hip_fail(hipError_t e, const char* what) {
+        if (err.empty()) err = std::string(what) + ": " + hipGetErrorString(e);
+        return fail(QS_EIO, "%s", err.c_str());
+    }
+};
+
+extern "C" {
+
+int qs_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline** out) {
+    qs_host::clear_error();
+    if (!out) return fail(QS_EINVAL, "null output handle");
+    *out = nullptr;
+    if (n_slots < 2 || n_slots > 16) return fail(QS_EINVAL, "n_slots %d outside [2, 16]", n_slots);
+    if (n_copy_threads < 1 || n_copy_threads > 64)
+        return fail(QS_EINVAL, "n_copy_threads %d outside [1, 64]", n_copy_threads);
+    const int ndev = qs_device_count();
+    if (device < 0 || device >= ndev)
+        return fail(QS_EINVAL, "device %d not present (%d ROCm devices visible)", device, ndev);
+    hipError_t e = hipSetDevice(device);
+    if (e != hipSuccess) return fail(QS_EIO, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
+    auto p = std::make_unique<qs_pipeline>();
+    p->device = device;
+    if ((e = hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&p->compute, hipStreamNonBlocking)) != hipSuccess) {
+        qs_pipeline_destroy(p.release());
+        return fail(QS_EIO, "stream creation failed: %s", hipGetErrorString(e));
+    }
+    p->slots.resize(n_slots);
+    for (auto& s : p->slots) {
+        if ((e = hipEventCreateWithFlags(&s.h2d, hipEventDisableTiming)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&s.kern, hipEventDisableTiming)) != hipSuccess ||
+            (e = hipEventCreateWithFlags(&s.d2h, hipEventDisableTiming)) != hipSuccess) {
+            qs_pipeline_destroy(p.release());
+            return fail(QS_EIO, "event creation failed: %s", hipGetErrorString(e));
+        }
+    }
+    p->pool = std::make_unique<CopyPool>(n_copy_threads);
+    p->writer = std::make_unique<Writer>(device);
+    *out = p.release();
+    return 0;
+}
+
+int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void* src, int64_t n_rows,
+                         int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
+                         int64_t out_offset) {
+    qs_host::clear_error();
+    if (!p) return fail(QS_EINVAL, "null pipeline");
+    if (int rc = p->check_writer()) return rc;
+    const int esz = elem_size(src_type);
+    if (!esz) return fail(QS_EINVAL, "unsupported source type %d (F32=0, F16=1, BF16=30)", src_type);
+    if (n_rows < 0 || rows_per_chunk <= 0 || out_offset < 0 || fd < 0)
+        return fail(QS_EINVAL, "bad n_rows %lld / rows_per_chunk %lld / offset %lld / fd %d",
+                    (long long)n_rows, (long long)rows_per_chunk, (long long)out_offset, fd);
+    if (!qs_type_supported(ggml_type)) return fail(QS_ENOTSUP, "ggml type %d has no HIP quantizer", ggml_type);
+    const int64_t out_row = qs_row_bytes(ggml_type, k);
+    if (out_row < 0) return (int)out_row;
+    if (n_rows == 0) return 0;
+    if (!src) return fail(QS_EINVAL, "null src");
+    if (qs_type_needs_imatrix(ggml_type) == 1 && !imatrix)
+        return fail(QS_EINVAL, "ggml type %d requires an imatrix", ggml_type);
+    const bool use_qw = imatrix && qs_type_uses_imatrix(ggml_type) == 1;
+    hipError_t e = hipSetDevice(p->device);
+    if (e != hipSuccess) return p->hip_fail(e, "hipSetDevice");
+    const int64_t in_row = k * esz;
+    const char* rows = static_cast<const char*>(src);
+
+    for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_chunk) {
+        const int64_t n = std::min(rows_per_chunk, n_rows - r0);
+        const size_t nin = (size_t)(n * in_row), nout = (size_t)(n * out_row), nqw = use_qw ? (size_t)k * 4 : 0;
+        Slot& s = p->slots[p->next];
+        p->next = (p->next + 1) % p->slots.size();
+        if (s.used) {
+            // in_pin: its H2D is done; out_pin: its write is done; device
+            // buffers: the kernel and the D2H that used them are done
+            if ((e = hipEventSynchronize(s.h2d)) != hipSuccess) return p->hip_fail(e, "H2D");
+            p->writer->wait(s.write_seq);
+            if (int rc = p->check_writer()) return rc;
+            if (s.x_dev.n < nin || s.out_dev.n < nout || s.qw_dev.n < nqw) {
+                if ((e = hipEventSynchronize(s.d2h)) != hipSuccess) return p->hip_fail(e, "D2H");
+            }
+        }
+        if (!s.in_pin.grow(nin) || !s.out_pin.grow(nout) || !s.qw_pin.grow(nqw) || !s.x_dev.grow(nin) ||
+            !s.out_dev.grow(nout) || !s.qw_dev.grow(nqw)) {
+            if (p->err.empty()) p->err = "out of memory staging a chunk";
+            return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)n,
+                        (long long)in_row);
+        }
+        // mapping -> pinned, in parts of at least kCopyPart bytes
+        const char* from = rows + r0 * in_row;
+        char* to = static_cast<char*>(s.in_pin.p);
+        const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), nin / kCopyPart));
+        std::vector<std::function<void()>> tasks;
+        for (size_t i = 0; i < parts; i++) {
+            const size_t a = nin * i / parts, b = nin * (i + 1) / parts;
+            tasks.emplace_back([=] { std::memcpy(to + a, from + a, b - a); });
+        }
+        p->pool->run(tasks);
+        if (nqw) std::memcpy(s.qw_pin.p, imatrix, nqw);
+
+        if (s.used && (e = hipStreamWaitEvent(p->copy, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(s.x_dev.p, s.in_pin.p, nin, hipMemcpyHostToDevice, p->copy)) != hipSuccess)
+            return p->hip_fail(e, "H2D");
+        if (nqw && (e = hipMemcpyAsync(s.qw_dev.p, s.qw_pin.p, nqw, hipMemcpyHostToDevice, p->copy)) != hipSuccess)
+            return p->hip_fail(e, "H2D");
+        if ((e = hipEventRecord(s.h2d, p->copy)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipStreamWaitEvent(p->compute, s.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if (s.used && (e = hipStreamWaitEvent(p->compute, s.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        const int rc = qs_quantize(ggml_type, src_type, s.x_dev.p, n, k, in_row,
+                                   nqw ? static_cast<const float*>(s.qw_dev.p) : nullptr, s.out_dev.p,
+                                   (int64_t)nout, p->compute);
+        if (rc) {
+            if (p->err.empty()) p->err = "quantizer launch failed";
+            return rc;
+        }
+        if ((e = hipEventRecord(s.kern, p->compute)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipStreamWaitEvent(p->copy, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(s.out_pin.p, s.out_dev.p, nout, hipMemcpyDeviceToHost, p->copy)) != hipSuccess)
+            return p->hip_fail(e, "D2H");
+        if ((e = hipEventRecord(s.d2h, p->copy)) != hipSuccess) return p->hip_fail(e, "event");
+        s.used = true;
+        s.write_seq = p->writer->push({s.d2h, s.out_pin.p, nout, fd, out_offset + r0 * out_row});
+    }
+    return 0;
+}
+
+int qs_pipeline_write(qs_pipeline* p, const void* src, int64_t nbytes, int fd, int64_t out_offset) {
+    qs_host::clear_error();
+    if (!p) return fail(QS_EINVAL, "null pipeline");
+    if (int rc = p->check_writer()) return rc;
+    if (nbytes < 0 || out_offset < 0 || fd < 0 || (nbytes && !src))
+        return fail(QS_EINVAL, "bad write of %lld bytes at %lld (fd %d)", (long long)nbytes,
+                    (long long)out_offset, fd);
+    if (nbytes) p->writer->push({nullptr, src, (size_t)nbytes, fd, out_offset});
+    return 0;
+}
+
+int qs_pipeline_finish(qs_pipeline* p) {
+    qs_host::clear_error();
+    if (!p) return fail(QS_EINVAL, "null pipeline");
+    p->writer->drain();
+    hipError_t e = hipSetDevice(p->device);
+    if (e == hipSuccess) e = hipStreamSynchronize(p->copy);
+    if (e == hipSuccess) e = hipStreamSynchronize(p->compute);
+    if (e != hipSuccess) return p->hip_fail(e, "device work failed");
+    return p->check_writer();
+}
+
+void qs_pipeline_destroy(qs_pipeline* p) {
+    if (!p) return;
+    if (p->writer) p->writer->drain();
+    (void)hipSetDevice(p->device);
+    if (p->copy) (void)hipStreamSynchronize(p->copy);
+    if (p->compute) (void)hipStreamSynchronize(p->compute);
+    p->writer.reset();
+    p->pool.reset();
+    for (auto& s : p->slots) {
+        s.in_pin.release();
+        s.out_pin.release();
+        s.qw_pin.release();
+        s.x_dev.release();
+        s.out_dev.release();
+        s.qw_dev.release();
+        if (s.h2d) (void)hipEventDestroy(s.h2d);
+        if (s.kern) (void)hipEventDestroy(s.kern);
+        if (s.d2h) (void)hipEventDestroy(s.d2h);
+    }
+    if (p->copy) (void)hipStreamDestroy(p->copy);
+    if (p->compute) (void)hipStreamDestroy(p->compute);
+    delete p;
+}
+
+}  // extern "C"

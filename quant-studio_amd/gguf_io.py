@@ -240,7 +240,16 @@ class GGUFWriter:
             hdr += b"".join(struct.pack("<Q", d) for d in ne)
             hdr += struct.pack("<IQ", int(gtype), off)
         self.fout.write(hdr)
+        self.data_start_offset = pad_to(len(hdr), self.alignment)
         return self.fout
+
+    def data_start(self) -> int:
+        """File offset of the tensor data section (after write_header)."""
+        return self.data_start_offset
+
+    def total_size(self) -> int:
+        """Size of the complete file: data section start + padded tensor data."""
+        return self.data_start_offset + self._offset
 
     def pad(self) -> None:
         pos = self.fout.tell()

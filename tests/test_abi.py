@@ -24,14 +24,16 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_api():
     names = set(declared_functions())
     assert {"qs_abi_version", "qs_row_bytes", "qs_quantize", "qs_last_error",
-            "qs_type_supported", "qs_type_needs_imatrix", "qs_type_uses_imatrix"} <= names
+            "qs_type_supported", "qs_type_needs_imatrix", "qs_type_uses_imatrix",
+            "qs_device_count", "qs_pipeline_create", "qs_pipeline_quantize", "qs_pipeline_write",
+            "qs_pipeline_finish", "qs_pipeline_destroy"} <= names
 
 
 def test_library_exports_every_declared_symbol(qs):
     L = qs.library()
     for name in declared_functions():
         assert hasattr(L, name), f"libqs_hip.so does not export {name}"
-    assert L.qs_abi_version() == 1
+    assert L.qs_abi_version() == qs.ABI_VERSION == 2
 
 
 @pytest.mark.parametrize("qtype", sorted(TYPES))
@@ -93,3 +95,20 @@ def test_quant_fn_refuses_cpu_tensors(qs):
     fn = qs.QUANT_TYPES["q4_k"].make_kernel(torch.device("cpu"), None)
     with pytest.raises(ValueError, match="ROCm device"):
         fn(torch.zeros(2, 256))
+
+
+def test_pipeline_rejects_bad_arguments_without_device_work(qs):
+    import ctypes
+    L = qs.library()
+    h = ctypes.c_void_p()
+    assert L.qs_pipeline_create(0, 1, 4, ctypes.byref(h)) == -22          # too few slots
+    assert "n_slots" in qs.last_error()
+    assert L.qs_pipeline_create(0, 3, 0, ctypes.byref(h)) == -22          # no copy threads
+    assert L.qs_pipeline_create(-1, 3, 4, ctypes.byref(h)) == -22         # no such device
+    assert "not present" in qs.last_error() and not h.value
+    assert L.qs_pipeline_create(0, 3, 4, None) == -22
+    assert L.qs_pipeline_quantize(None, 12, 30, None, 1, 256, None, 1, 1, 0) == -22
+    assert L.qs_pipeline_write(None, None, 0, 1, 0) == -22
+    assert L.qs_pipeline_finish(None) == -22
+    L.qs_pipeline_destroy(None)
+    assert L.qs_device_count() >= 0

@@ -83,3 +83,41 @@ def test_schemes_with_imatrix(tmp_path, scheme, ftype, extra):
     out = tmp_path / "o.gguf"
     run_cli(src, out, scheme, "--imatrix", im, "--mem", "128K", *extra)
     check_output(src, out, expect, ftype=ftype, imatrix=imat)
+
+
+def test_pipeline_chunks_match_single_call_and_report_write_errors(tmp_path):
+    """The native pipeline directly: any chunking writes the same bytes as one
+    qs_quantize call (checked against the oracle), and a failing write (here a
+    read-only descriptor) surfaces as an error no later than finish()."""
+    import os
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    rng = np.random.default_rng(7)
+    x = (rng.normal(size=(37, 512)) * 0.02).astype(np.float32)
+    qw = rng.lognormal(size=512).astype(np.float32)
+    ref = oracle.quantize("q4_k", x, qw)
+    info = io.TensorInfo("t", (512, 37), GT.F32, 0, x.nbytes, x.view(np.uint8).reshape(-1))
+    for rows_per_chunk in (1, 5, 37, 100):
+        path = tmp_path / f"o{rows_per_chunk}.bin"
+        fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+        try:
+            with pl.NativePipeline(0, fd) as p:
+                p.write(np.frombuffer(b"HEAD", np.uint8), 0)
+                p.quantize_tensor(info, int(GT.Q4_K), qw, rows_per_chunk, 64, qs.row_bytes(int(GT.Q4_K), 512))
+                p.finish()
+        finally:
+            os.close(fd)
+        b = path.read_bytes()
+        assert b[:4] == b"HEAD" and b[4:64] == bytes(60)
+        assert np.array_equal(np.frombuffer(b[64:], np.uint8).reshape(ref.shape), ref), rows_per_chunk
+    ro = tmp_path / "ro.bin"
+    ro.write_bytes(b"")
+    fd = os.open(ro, os.O_RDONLY)
+    try:
+        with pl.NativePipeline(0, fd) as p:
+            # reported by a later queue call once the writer has failed, else by finish()
+            with pytest.raises(pl.PipelineError, match="write failed"):
+                p.quantize_tensor(info, int(GT.Q4_K), qw, 8, 0, qs.row_bytes(int(GT.Q4_K), 512))
+                p.finish()
+    finally:
+        os.close(fd)
