@@ -93,7 +93,7 @@ struct HostTab {
 // levels 0..2, IQ3: 0..7), the grid points within its nwant smallest distinct
 // squared distances in (distance, index) order -- the neighbour tables of
 // iq2.py:31-74, iq2xs_common.py:41-95, iq3_common.py:29-68.
-HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant) {
+HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int maxch) {
     const int nsub = bits == 2 ? 8 : 4, lmask = (1 << bits) - 1, lmax = bits == 2 ? 2 : 7;
     const int ksize = bits == 2 ? 43692 : 4096;
     HostTab t;
@@ -135,7 +135,7 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant) {
         const size_t len = t.nbr.size() - start;
         t.nbr.resize((t.nbr.size() + 7) / 8 * 8, 0);
         t.cinfo[c] = (uint32_t)((start / 8) << 12) | (uint32_t)len;
-        t.ok = t.ok && len < 4096 && start / 8 < (1u << 19);
+        t.ok = t.ok && len < 4096 && start / 8 < (1u << 19) && (maxch == 0 || len <= 8u * maxch);
     }
     if (bits == 3) {
         // 16-bit map and length-prefixed lists; positions must fit in 15 bits
@@ -159,11 +159,11 @@ const HostTab& host_tab(int id) {
     static std::once_flag once;
     static std::array<HostTab, IQT_N> tabs;
     std::call_once(once, [] {
-        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2);
-        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2);
-        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1);
-        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2);
-        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3);
+        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_256_MAXCH);
+        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_512_MAXCH);
+        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_1024_MAXCH);
+        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2, 0);
+        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3, 0);
     });
     return tabs[id];
 }

@@ -38,6 +38,10 @@ struct IqTabDev {
 constexpr uint32_t CI_ON_GRID = 0x80000000u;
 constexpr uint32_t K16_ON_GRID = 0x8000u;
 
+// most 8-candidate chunks in one neighbour list of each IQ2 grid (longest
+// lists 150, 292 and 70 entries; checked when the tables are built)
+constexpr int IQ2_256_MAXCH = 19, IQ2_512_MAXCH = 37, IQ2_1024_MAXCH = 9;
+
 // LDS of the IQ kernels: x^2 staging for the superblock sum, per-group
 // scales, and the packed output blocks.
 template <int SPW, int BYTES>
@@ -149,6 +153,95 @@ QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const uint16_t* k
         }
     }
     return bi;
+}
+
+// Wave-balanced projection of subgroup OFF..OFF+NV-1 of every lane's group
+// (IQ2 grids; same arithmetic and result as iq_project). The off-grid lanes'
+// neighbour lists are cut into chunks of 8 candidates and the wave's chunks
+// are dealt to all 64 lanes in turn, so a long list no longer holds the whole
+// wave: a chunk's lane fetches the owner's values and scale with ds_bpermute,
+// evaluates the 8 candidates in list order and merges its first minimum into
+// the owner's LDS slot as a 64-bit key (distance bits, list position, grid
+// index): the least key is the list's first minimum, as in the reference's
+// sequential scan. Every lane of the wave must call this together; lanes
+// with want == false take part but search nothing (their result is unused).
+//   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
+//   res:  LDS, 64 keys
+template <int NV, int OFF, int N, int MAXCH>
+QS_DEV int iq2_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cmap, unsigned long long* res,
+                            const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool want,
+                            bool& on) {
+    const int lane = threadIdx.x;
+    int code = 0;
+#pragma unroll
+    for (int j = 0; j < NV; j++) {
+        float t = inv * xv[OFF + j];
+        t = t - 1.0f;
+        t = 0.5f * t;
+        code |= (int)clampf(rintf(t), 0.0f, 2.0f) << (2 * j);
+    }
+    const uint32_t ci = T.cinfo[code];
+    on = (ci & CI_ON_GRID) != 0;
+    const int n = (on || !want) ? 0 : (int)(ci & 0xfffu);
+    const int nch = (n + 7) >> 3;
+    int incl = nch;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d);
+        if (lane >= d) incl += t;
+    }
+    const int excl = incl - nch;
+    const int total = __shfl(incl, 63);
+    for (int i = 0; i < nch; i++) cmap[excl + i] = (uint8_t)lane;
+    res[lane] = ~0ull;
+    wave_sync();
+    const uint4* lists = reinterpret_cast<const uint4*>(T.nbr);
+    for (int base = 0; base < total; base += 64) {
+        const int c = base + lane;
+        const bool have = c < total;
+        const int owner = have ? (int)cmap[c] : lane;
+        const int o_excl = __shfl(excl, owner);
+        const uint32_t o_ci = (uint32_t)__shfl((int)ci, owner);
+        const float o_sc = __shfl(sc, owner);
+        float xs[NV], ws[NV];
+#pragma unroll
+        for (int e = 0; e < NV; e++) {
+            xs[e] = __shfl(xv[OFF + e], owner);
+            ws[e] = __shfl(wv[OFF + e], owner);
+        }
+        if (have) {
+            const int kc = c - o_excl;
+            const int o_n = (int)(o_ci & 0xfffu);
+            const uint4 q = lists[((o_ci >> 12) & 0x7ffffu) + kc];
+            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+            unsigned long long best = ~0ull;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int pos = 8 * kc + j;
+                if (pos < o_n) {
+                    const int gi = (int)((w4[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    const uint32_t gc = glds[gi];
+                    float d2 = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < NV; e++) {
+                        float diff = o_sc * grid_value<2>(gc, e);
+                        diff = diff - xs[e];
+                        const float t = (ws[e] * diff) * diff;
+                        d2 = d2 + t;
+                    }
+                    const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
+                                                   ((unsigned long long)pos << 16) | (unsigned)gi;
+                    best = key < best ? key : best;
+                }
+            }
+            atomicMin(&res[owner], best);
+        }
+    }
+    wave_sync();
+    if (on) return (int)(ci & 0xffffu);
+    const unsigned long long r = res[lane];
+    // no finite distance: the sequential scan keeps its initial -1
+    return (uint32_t)(r >> 32) >= 0x7f800000u ? -1 : (int)(r & 0xffffu);
 }
 
 // sign-parity fold of 8 values (iq2.py:438-450): |x|, the smallest (w*x)*x
@@ -291,6 +384,8 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
     constexpr int LPS = 8, SPW = 8, BYTES = 66;
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[256];
+    __shared__ uint8_t cmap[64 * IQ2_256_MAXCH];
+    __shared__ unsigned long long res[64];
     for (int i = threadIdx.x; i < 256; i += 64) glds[i] = T.grid[i];
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
@@ -319,7 +414,9 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         const float sc = 1.0f / inv;
         int gi[4];
         bool on;
-        static_for<0, 4>([&](auto S) { gi[S] = iq_project<2, 8, 8 * S>(T, glds, nullptr, xval, waux, inv, sc, on); });
+        static_for<0, 4>([&](auto S) {
+            gi[S] = iq2_project_wave<8, 8 * S, 32, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on);
+        });
         iq_sums<2, 8, 4>(glds, gi, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -335,7 +432,9 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         const float inv = 1.0f / (proj ? scale : 1.0f);
         int gp[4];
         bool on;
-        static_for<0, 4>([&](auto S) { gp[S] = iq_project<2, 8, 8 * S>(T, glds, nullptr, xval, waux, inv, scale, on); });
+        static_for<0, 4>([&](auto S) {
+            gp[S] = iq2_project_wave<8, 8 * S, 32, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, scale, proj, on);
+        });
         iq_sums<2, 8, 4>(glds, gp, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
         if (proj && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
@@ -388,6 +487,9 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[GS];
     __shared__ int wlds[SPW][16][2];
+    constexpr int MAXCH = IS_S ? IQ2_1024_MAXCH : IQ2_512_MAXCH;
+    __shared__ uint8_t cmap[64 * MAXCH];
+    __shared__ unsigned long long res[64];
     for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
     const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
@@ -417,8 +519,8 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         const float inv = rdiv(sweep.v[st], gsafe), sc = 1.0f / inv;
         int gi[2];
         bool on[2];
-        gi[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, sc, on[0]);
-        gi[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, sc, on[1]);
+        gi[0] = iq2_project_wave<8, 0, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[0]);
+        gi[1] = iq2_project_wave<8, 8, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[1]);
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -432,11 +534,19 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         }
     }
     const bool need = active && scale > 0 && !(og[0] && og[1]);
-    if (need) {
-        const float inv = 1.0f / scale;
+    {
+        // every lane takes part in the wave search; only off-grid winners of
+        // lanes that need it are searched and replaced
+        const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
-        if (!og[0]) win[0] = iq_project<2, 8, 0>(T, glds, nullptr, xval, waux, inv, scale, on);
-        if (!og[1]) win[1] = iq_project<2, 8, 8>(T, glds, nullptr, xval, waux, inv, scale, on);
+        const int r0 = iq2_project_wave<8, 0, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
+                                                         need && !og[0], on);
+        const int r1 = iq2_project_wave<8, 8, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
+                                                         need && !og[1], on);
+        if (need && !og[0]) win[0] = r0;
+        if (need && !og[1]) win[1] = r1;
+    }
+    if (need) {
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, win, w, xval, sumqx, sumq2);
         if (sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
