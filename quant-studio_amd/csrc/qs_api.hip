@@ -84,7 +84,6 @@ enum IqTabId { IQT_G2_256, IQT_G2_512, IQT_G2_1024, IQT_G3_256, IQT_G3_512, IQT_
 struct HostTab {
     std::vector<uint16_t> grid, nbr;
     std::vector<uint32_t> cinfo;       // IQ2 layout described at qs::IqTabDev
-    std::vector<uint16_t> kmap16, lnbr;   // IQ3 layout described at qs::IqTabDev
     int code0 = 0;
     bool ok = true;
 };
@@ -93,7 +92,7 @@ struct HostTab {
 // levels 0..2, IQ3: 0..7), the grid points within its nwant smallest distinct
 // squared distances in (distance, index) order -- the neighbour tables of
 // iq2.py:31-74, iq2xs_common.py:41-95, iq3_common.py:29-68.
-HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int maxch) {
+HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch, int maxch) {
     const int nsub = bits == 2 ? 8 : 4, lmask = (1 << bits) - 1, lmax = bits == 2 ? 2 : 7;
     const int ksize = bits == 2 ? 43692 : 4096;
     HostTab t;
@@ -128,29 +127,14 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ma
         std::sort(dist.begin(), dist.end());
         dist.erase(std::unique(dist.begin(), dist.end()), dist.end());
         const int limit = dist[std::min<int>(nwant, (int)dist.size()) - 1];
-        const size_t start = t.nbr.size();     // a multiple of 8: 16-byte aligned
+        const size_t start = t.nbr.size();     // a multiple of ch: one aligned vector per chunk
         for (int rank = 0; rank < (int)dist.size() && dist[rank] <= limit; rank++)
             for (int i = 0; i < gs; i++)
                 if (d2[i] == dist[rank]) t.nbr.push_back((uint16_t)i);
         const size_t len = t.nbr.size() - start;
-        t.nbr.resize((t.nbr.size() + 7) / 8 * 8, 0);
-        t.cinfo[c] = (uint32_t)((start / 8) << 12) | (uint32_t)len;
-        t.ok = t.ok && len < 4096 && start / 8 < (1u << 19) && (maxch == 0 || len <= 8u * maxch);
-    }
-    if (bits == 3) {
-        // 16-bit map and length-prefixed lists; positions must fit in 15 bits
-        t.kmap16.assign(ksize, 0);
-        for (int c = 0; c < ksize; c++) {
-            if (t.cinfo[c] & qs::CI_ON_GRID) {
-                t.kmap16[c] = (uint16_t)(qs::K16_ON_GRID | (t.cinfo[c] & 0xffffu));
-                continue;
-            }
-            const size_t pos = t.lnbr.size(), len = t.cinfo[c] & 0xfffu, st = 8 * (size_t)(t.cinfo[c] >> 12);
-            t.ok = t.ok && pos < qs::K16_ON_GRID;
-            t.kmap16[c] = (uint16_t)pos;
-            t.lnbr.push_back((uint16_t)len);
-            t.lnbr.insert(t.lnbr.end(), t.nbr.begin() + st, t.nbr.begin() + st + len);
-        }
+        t.nbr.resize((t.nbr.size() + ch - 1) / ch * ch, 0);
+        t.cinfo[c] = (uint32_t)((start / ch) << 12) | (uint32_t)len;
+        t.ok = t.ok && len < 4096 && start / ch < (1u << 19) && len <= (size_t)ch * maxch;
     }
     return t;
 }
@@ -159,11 +143,11 @@ const HostTab& host_tab(int id) {
     static std::once_flag once;
     static std::array<HostTab, IQT_N> tabs;
     std::call_once(once, [] {
-        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_256_MAXCH);
-        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_512_MAXCH);
-        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_1024_MAXCH);
-        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2, 0);
-        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3, 0);
+        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_CH, qs::IQ2_256_MAXCH);
+        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_CH, qs::IQ2_512_MAXCH);
+        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_CH, qs::IQ2_1024_MAXCH);
+        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2, qs::IQ3_CH, qs::IQ3_256_MAXCH);
+        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3, qs::IQ3_CH, qs::IQ3_512_MAXCH);
     });
     return tabs[id];
 }
@@ -195,10 +179,8 @@ bool device_tabs(std::array<qs::IqTabDev, IQT_N>& out) {
             d[id].grid = upload(h.grid);
             d[id].cinfo = upload(h.cinfo);
             d[id].nbr = upload(h.nbr);
-            d[id].kmap16 = upload(h.kmap16);
-            d[id].lnbr = upload(h.lnbr);
             d[id].code0 = h.code0;
-            if (!h.ok || !d[id].grid || !d[id].cinfo || !d[id].nbr || !d[id].kmap16 || !d[id].lnbr) return false;
+            if (!h.ok || !d[id].grid || !d[id].cinfo || !d[id].nbr) return false;
         }
         it = g_dev_tabs.emplace(dev, d).first;
     }

@@ -18,29 +18,27 @@
 namespace qs {
 
 // Device copy of one grid's tables (built once per device on the host).
-// IQ2 grids: cinfo packs everything a projection needs about a code:
+// cinfo packs everything a projection needs about a code:
 //   on-grid:  bit 31 set, bits 0..15 = grid index;
-//   off-grid: bits 12..30 = first neighbour / 8, bits 0..11 = list length;
-// each list starts on a 16-byte boundary of nbr, so a lane fetches eight
-// candidates with one vector load.
-// IQ3 grids (4096 codes, short lists): kmap16 fits in LDS at 2 bytes a code,
-//   on-grid:  bit 15 set, bits 0..14 = grid index;
-//   off-grid: position of the code's list in lnbr, stored as [len, i0, i1 ...].
+//   off-grid: bits 12..30 = first neighbour / CH, bits 0..11 = list length;
+// each list starts on a CH-entry boundary of nbr and is padded to a multiple
+// of CH, so a lane fetches a chunk of CH candidates with one vector load
+// (CH = 8 for the IQ2 grids, 4 for the IQ3 grids, whose lists are short).
 struct IqTabDev {
     const uint16_t* grid;     // grid codes (BITS-bit levels per value)
-    const uint32_t* cinfo;    // IQ2: code -> packed kmap / list position / length
-    const uint16_t* nbr;      // IQ2: neighbour grid indices, (distance, index) order
-    const uint16_t* kmap16;   // IQ3: code -> grid index | list position
-    const uint16_t* lnbr;     // IQ3: length-prefixed neighbour lists
+    const uint32_t* cinfo;    // code -> packed kmap / list position / length
+    const uint16_t* nbr;      // neighbour grid indices, (distance, index) order
     int code0;                // grid index of the all-zero code (0 if off-grid)
 };
 
 constexpr uint32_t CI_ON_GRID = 0x80000000u;
-constexpr uint32_t K16_ON_GRID = 0x8000u;
 
-// most 8-candidate chunks in one neighbour list of each IQ2 grid (longest
-// lists 150, 292 and 70 entries; checked when the tables are built)
+// candidates per chunk, and the most chunks in one neighbour list of each
+// grid (longest lists: IQ2 150 / 292 / 70, IQ3 36 / 38 entries; checked when
+// the tables are built)
+constexpr int IQ2_CH = 8, IQ3_CH = 4;
 constexpr int IQ2_256_MAXCH = 19, IQ2_512_MAXCH = 37, IQ2_1024_MAXCH = 9;
+constexpr int IQ3_256_MAXCH = 9, IQ3_512_MAXCH = 10;
 
 // LDS of the IQ kernels: x^2 staging for the superblock sum, per-group
 // scales, and the packed output blocks.
@@ -72,16 +70,32 @@ QS_DEV float grid_value(uint32_t gcode, int j) {
     return (float)(2 * ((gcode >> (BITS * j)) & ((1u << BITS) - 1u)) + 1);
 }
 
-// Project one subgroup (values OFF..OFF+NV-1 of the lane's group) at the
-// candidate scale: levels clamp(round(0.5*(inv*x - 1)), 0, LMAX), then the
-// kmap, then the first-minimum weighted distance over the neighbour list
-// (iq2.py:347-372, iq2xs_common.py:222-271, iq3_common.py:209-256).
-// IQ2 distances are a left-to-right sum of 8 terms from +0; IQ3's are
+
+// Project subgroup OFF..OFF+NV-1 of every lane's group at its candidate scale
+// (iq2.py:347-372, iq2xs_common.py:222-271, iq3_common.py:209-256): levels
+// clamp(round(0.5*(inv*x - 1)), 0, LMAX) -> code -> kmap hit, or the first
+// minimum of the weighted distance over the code's neighbour list. IQ2
+// distances are a left-to-right sum of 8 terms from +0; IQ3's are
 // ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and diff = sc*g - x.
-template <int BITS, int NV, int OFF, int N>
-QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const uint16_t* kmap_lds,
-                      const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool& on) {
+//
+// The search is wave-balanced: the off-grid lanes' lists are cut into chunks
+// of CH candidates and the wave's chunks are dealt to all 64 lanes in turn, so
+// one long list no longer holds the whole wave. A chunk's lane fetches the
+// owner's values and scale with ds_bpermute, evaluates its candidates in list
+// order and merges its first minimum into the owner's LDS slot as a 64-bit key
+// (distance bits, list position, grid index); the least key is the list's
+// first minimum, the result of the reference's sequential scan. Every lane of
+// the wave calls this together; lanes with want == false take part but search
+// nothing (their result is unused).
+//   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
+//   res:  LDS, 64 keys
+template <int BITS, int NV, int OFF, int CH, int MAXCH, int N>
+QS_DEV int iq_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cmap, unsigned long long* res,
+                           const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool want,
+                           bool& on) {
+    static_assert(CH == 4 || CH == 8, "chunks are one 8- or 16-byte load");
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
+    const int lane = threadIdx.x;
     int code = 0;
 #pragma unroll
     for (int j = 0; j < NV; j++) {
@@ -90,100 +104,10 @@ QS_DEV int iq_project(const IqTabDev& T, const uint16_t* glds, const uint16_t* k
         t = 0.5f * t;
         code |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
     }
-    float best = __builtin_inff();
-    int bi = -1;
-    if constexpr (BITS == 3) {
-        // short lists (about five entries): one candidate per iteration, the
-        // next index loaded while this one is evaluated
-        const uint32_t k16 = kmap_lds[code];
-        on = (k16 & K16_ON_GRID) != 0;
-        if (on) return (int)(k16 & 0x7fffu);
-        const uint16_t* lp = T.lnbr + k16;
-        const int n = lp[0];
-        int gi = lp[1];
-        for (int k = 0; k < n; k++) {
-            const int nxt = (k + 1 < n) ? (int)lp[k + 2] : 0;
-            const uint32_t gc = glds[gi];
-            float d2 = 0.0f;
-#pragma unroll
-            for (int e = 0; e < NV; e++) {
-                float diff = sc * grid_value<BITS>(gc, e);
-                diff = diff - xv[OFF + e];
-                const float t = (wv[OFF + e] * diff) * diff;
-                d2 = (e == 0) ? t : d2 + t;
-            }
-            if (d2 < best) {
-                best = d2;
-                bi = gi;
-            }
-            gi = nxt;
-        }
-    } else {
-        // IQ2 lists are long (tens of entries): eight indices per 16-byte load,
-        // the next eight in flight while these are evaluated
-        const uint32_t ci = T.cinfo[code];
-        on = (ci & CI_ON_GRID) != 0;
-        if (on) return (int)(ci & 0xffffu);
-        const int n = (int)(ci & 0xfffu);
-        const uint4* lp = reinterpret_cast<const uint4*>(T.nbr) + ((ci >> 12) & 0x7ffffu);
-        uint4 nxt = lp[0];
-        for (int k = 0; k < n; k += 8) {
-            const uint4 c = nxt;
-            if (k + 8 < n) nxt = lp[(k >> 3) + 1];
-            const uint32_t w4[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                if (k + j < n) {
-                    const int gi = (int)((w4[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    const uint32_t gc = glds[gi];
-                    float d2 = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < NV; e++) {
-                        float diff = sc * grid_value<BITS>(gc, e);
-                        diff = diff - xv[OFF + e];
-                        const float t = (wv[OFF + e] * diff) * diff;
-                        d2 = d2 + t;
-                    }
-                    if (d2 < best) {
-                        best = d2;
-                        bi = gi;
-                    }
-                }
-            }
-        }
-    }
-    return bi;
-}
-
-// Wave-balanced projection of subgroup OFF..OFF+NV-1 of every lane's group
-// (IQ2 grids; same arithmetic and result as iq_project). The off-grid lanes'
-// neighbour lists are cut into chunks of 8 candidates and the wave's chunks
-// are dealt to all 64 lanes in turn, so a long list no longer holds the whole
-// wave: a chunk's lane fetches the owner's values and scale with ds_bpermute,
-// evaluates the 8 candidates in list order and merges its first minimum into
-// the owner's LDS slot as a 64-bit key (distance bits, list position, grid
-// index): the least key is the list's first minimum, as in the reference's
-// sequential scan. Every lane of the wave must call this together; lanes
-// with want == false take part but search nothing (their result is unused).
-//   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
-//   res:  LDS, 64 keys
-template <int NV, int OFF, int N, int MAXCH>
-QS_DEV int iq2_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cmap, unsigned long long* res,
-                            const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool want,
-                            bool& on) {
-    const int lane = threadIdx.x;
-    int code = 0;
-#pragma unroll
-    for (int j = 0; j < NV; j++) {
-        float t = inv * xv[OFF + j];
-        t = t - 1.0f;
-        t = 0.5f * t;
-        code |= (int)clampf(rintf(t), 0.0f, 2.0f) << (2 * j);
-    }
     const uint32_t ci = T.cinfo[code];
     on = (ci & CI_ON_GRID) != 0;
     const int n = (on || !want) ? 0 : (int)(ci & 0xfffu);
-    const int nch = (n + 7) >> 3;
+    const int nch = (n + CH - 1) / CH;
     int incl = nch;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -195,7 +119,6 @@ QS_DEV int iq2_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cm
     for (int i = 0; i < nch; i++) cmap[excl + i] = (uint8_t)lane;
     res[lane] = ~0ull;
     wave_sync();
-    const uint4* lists = reinterpret_cast<const uint4*>(T.nbr);
     for (int base = 0; base < total; base += 64) {
         const int c = base + lane;
         const bool have = c < total;
@@ -212,22 +135,30 @@ QS_DEV int iq2_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cm
         if (have) {
             const int kc = c - o_excl;
             const int o_n = (int)(o_ci & 0xfffu);
-            const uint4 q = lists[((o_ci >> 12) & 0x7ffffu) + kc];
-            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+            const size_t chunk = ((o_ci >> 12) & 0x7ffffu) + (size_t)kc;
+            uint32_t wd[CH / 2];
+            if constexpr (CH == 8) {
+                const uint4 q = reinterpret_cast<const uint4*>(T.nbr)[chunk];
+                wd[0] = q.x; wd[1] = q.y; wd[2] = q.z; wd[3] = q.w;
+            } else {
+                const uint2 q = reinterpret_cast<const uint2*>(T.nbr)[chunk];
+                wd[0] = q.x; wd[1] = q.y;
+            }
             unsigned long long best = ~0ull;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int pos = 8 * kc + j;
+            for (int j = 0; j < CH; j++) {
+                const int pos = CH * kc + j;
                 if (pos < o_n) {
-                    const int gi = (int)((w4[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    const int gi = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
                     const uint32_t gc = glds[gi];
                     float d2 = 0.0f;
 #pragma unroll
                     for (int e = 0; e < NV; e++) {
-                        float diff = o_sc * grid_value<2>(gc, e);
+                        float diff = o_sc * grid_value<BITS>(gc, e);
                         diff = diff - xs[e];
                         const float t = (ws[e] * diff) * diff;
-                        d2 = d2 + t;
+                        if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
+                        else d2 = d2 + t;
                     }
                     const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
                                                    ((unsigned long long)pos << 16) | (unsigned)gi;
@@ -415,7 +346,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         int gi[4];
         bool on;
         static_for<0, 4>([&](auto S) {
-            gi[S] = iq2_project_wave<8, 8 * S, 32, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on);
+            gi[S] = iq_project_wave<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on);
         });
         iq_sums<2, 8, 4>(glds, gi, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
@@ -433,7 +364,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         int gp[4];
         bool on;
         static_for<0, 4>([&](auto S) {
-            gp[S] = iq2_project_wave<8, 8 * S, 32, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, scale, proj, on);
+            gp[S] = iq_project_wave<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, scale, proj, on);
         });
         iq_sums<2, 8, 4>(glds, gp, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
@@ -519,8 +450,8 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         const float inv = rdiv(sweep.v[st], gsafe), sc = 1.0f / inv;
         int gi[2];
         bool on[2];
-        gi[0] = iq2_project_wave<8, 0, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[0]);
-        gi[1] = iq2_project_wave<8, 8, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[1]);
+        gi[0] = iq_project_wave<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[0]);
+        gi[1] = iq_project_wave<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[1]);
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -539,9 +470,9 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         // lanes that need it are searched and replaced
         const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
-        const int r0 = iq2_project_wave<8, 0, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
+        const int r0 = iq_project_wave<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
                                                          need && !og[0], on);
-        const int r1 = iq2_project_wave<8, 8, 16, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
+        const int r1 = iq_project_wave<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
                                                          need && !og[1], on);
         if (need && !og[0]) win[0] = r0;
         if (need && !og[1]) win[1] = r1;
@@ -613,10 +544,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
     constexpr int LPS = 8, SPW = 8, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ uint16_t glds[GS];
-    __shared__ uint16_t klds[4096];
     __shared__ int act_lds[SPW][8];
+    constexpr int MAXCH = IS_S ? IQ3_512_MAXCH : IQ3_256_MAXCH;
+    __shared__ uint8_t cmap[64 * MAXCH];
+    __shared__ unsigned long long res[64];
     for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
-    for (int i = threadIdx.x; i < 4096; i += 64) klds[i] = T.kmap16[i];
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
@@ -642,13 +574,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
         Wg[k] = 0;
         og[k] = !IS_S;
     }
-    wave_sync();   // glds / klds ready
+    wave_sync();   // glds ready
 #pragma unroll 1
     for (int st = 0; st < steps.n; st++) {
         const float inv = rdiv(steps.v[st], gsafe), sc = 1.0f / inv;
         int gi[8];
         bool on[8];
-        static_for<0, 8>([&](auto S) { gi[S] = iq_project<3, 4, 4 * S>(T, glds, klds, xval, waux, inv, sc, on[S]); });
+        static_for<0, 8>([&](auto S) {
+            gi[S] = iq_project_wave<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[S]);
+        });
         float sumqx, sumq2;
         iq_tree_sums<3, 4, 8>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -670,7 +604,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
         const float inv2 = 1.0f / (redo ? scale : 1.0f);
         int w2[8];
         bool on[8];
-        static_for<0, 8>([&](auto S) { w2[S] = iq_project<3, 4, 4 * S>(T, glds, klds, xval, waux, inv2, scale, on[S]); });
+        static_for<0, 8>([&](auto S) {
+            w2[S] = iq_project_wave<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv2, scale,
+                                                                redo && (IS_S || !og[S]), on[S]);
+        });
 #pragma unroll
         for (int k = 0; k < 8; k++)
             if (redo && (IS_S || !og[k])) Wg[k] = w2[k];
