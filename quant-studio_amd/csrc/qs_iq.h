@@ -65,9 +65,44 @@ QS_DEV void static_for(F&& f) {
     }
 }
 
-template <int BITS>
-QS_DEV float grid_value(uint32_t gcode, int j) {
-    return (float)(2 * ((gcode >> (BITS * j)) & ((1u << BITS) - 1u)) + 1);
+// Grid levels staged in LDS as bytes 2l+1 (4 per word, NV/4 words per grid
+// point), so a level is one byte-to-float conversion.
+template <int BITS, int NV, int GS>
+QS_DEV void stage_levels(const uint16_t* grid, uint32_t* glv) {
+    constexpr int W = NV / 4;
+    for (int i = threadIdx.x; i < GS * W; i += 64) {
+        const uint32_t code = grid[i / W];
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int e = 4 * (i % W) + b;
+            word |= (2u * ((code >> (BITS * e)) & ((1u << BITS) - 1u)) + 1u) << (8 * b);
+        }
+        glv[i] = word;
+    }
+}
+
+template <int NV>
+struct Levels {
+    uint32_t w[NV / 4];
+};
+
+template <int NV>
+QS_DEV Levels<NV> grid_levels(const uint32_t* glv, int gi) {
+    Levels<NV> L;
+    if constexpr (NV == 8) {
+        const uint2 q = reinterpret_cast<const uint2*>(glv)[gi];
+        L.w[0] = q.x;
+        L.w[1] = q.y;
+    } else {
+        L.w[0] = glv[gi];
+    }
+    return L;
+}
+
+template <int NV>
+QS_DEV float level(const Levels<NV>& L, int e) {
+    return (float)((L.w[e >> 2] >> (8 * (e & 3))) & 0xffu);
 }
 
 
@@ -90,7 +125,7 @@ QS_DEV float grid_value(uint32_t gcode, int j) {
 //   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
 //   res:  LDS, 64 keys
 template <int BITS, int NV, int OFF, int CH, int MAXCH, int N>
-QS_DEV int iq_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cmap, unsigned long long* res,
+QS_DEV int iq_project_wave(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, unsigned long long* res,
                            const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool want,
                            bool& on) {
     static_assert(CH == 4 || CH == 8, "chunks are one 8- or 16-byte load");
@@ -150,11 +185,11 @@ QS_DEV int iq_project_wave(const IqTabDev& T, const uint16_t* glds, uint8_t* cma
                 const int pos = CH * kc + j;
                 if (pos < o_n) {
                     const int gi = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    const uint32_t gc = glds[gi];
+                    const Levels<NV> gl = grid_levels<NV>(glds, gi);
                     float d2 = 0.0f;
 #pragma unroll
                     for (int e = 0; e < NV; e++) {
-                        float diff = o_sc * grid_value<BITS>(gc, e);
+                        float diff = o_sc * level<NV>(gl, e);
                         diff = diff - xs[e];
                         const float t = (ws[e] * diff) * diff;
                         if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
@@ -217,14 +252,14 @@ QS_DEV int sign_bits8(const float (&x)[N], float (&xval)[N]) {
 
 // sums of (w*xval)*q and (w*q)*q over the lane's group for grid winners gi[]
 template <int BITS, int NV, int NSUB, int N>
-QS_DEV void iq_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
+QS_DEV void iq_sums(const uint32_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
                     float (&a)[N], float (&b)[N]) {
 #pragma unroll
     for (int s = 0; s < NSUB; s++) {
-        const uint32_t gc = glds[gi[s]];
+        const Levels<NV> gl = grid_levels<NV>(glds, gi[s]);
 #pragma unroll
         for (int j = 0; j < NV; j++) {
-            const float q = grid_value<BITS>(gc, j);
+            const float q = level<NV>(gl, j);
             a[NV * s + j] = (w[NV * s + j] * xval[NV * s + j]) * q;
             b[NV * s + j] = (w[NV * s + j] * q) * q;
         }
@@ -236,17 +271,17 @@ QS_DEV void iq_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w
 // a tree over the NSUB subgroup sums; reducing per subgroup keeps 2*NSUB
 // partials live instead of 2*N products
 template <int BITS, int NV, int NSUB, int N>
-QS_DEV void iq_tree_sums(const uint16_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
+QS_DEV void iq_tree_sums(const uint32_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
                          float& sumqx, float& sumq2) {
     static_assert(NV * NSUB == N && (NV & (NV - 1)) == 0, "subgroups must tile the group");
     float sa[NSUB], sb[NSUB];
 #pragma unroll
     for (int s = 0; s < NSUB; s++) {
-        const uint32_t gc = glds[gi[s]];
+        const Levels<NV> gl = grid_levels<NV>(glds, gi[s]);
         float a[NV], b[NV];
 #pragma unroll
         for (int j = 0; j < NV; j++) {
-            const float q = grid_value<BITS>(gc, j);
+            const float q = level<NV>(gl, j);
             a[j] = (w[NV * s + j] * xval[NV * s + j]) * q;
             b[j] = (w[NV * s + j] * q) * q;
         }
@@ -314,10 +349,10 @@ template <int SRC>
 __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4, IqSteps sweep) {
     constexpr int LPS = 8, SPW = 8, BYTES = 66;
     __shared__ IqLds<SPW, BYTES> s;
-    __shared__ uint16_t glds[256];
+    __shared__ __align__(16) uint32_t glds[256 * 2];
     __shared__ uint8_t cmap[64 * IQ2_256_MAXCH];
     __shared__ unsigned long long res[64];
-    for (int i = threadIdx.x; i < 256; i += 64) glds[i] = T.grid[i];
+    stage_levels<2, 8, 256>(T.grid, glds);
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
@@ -416,12 +451,12 @@ template <int SRC, bool IS_S>
 __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
     constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 82 : 74, GS = IS_S ? 1024 : 512;
     __shared__ IqLds<SPW, BYTES> s;
-    __shared__ uint16_t glds[GS];
+    __shared__ __align__(16) uint32_t glds[GS * 2];
     __shared__ int wlds[SPW][16][2];
     constexpr int MAXCH = IS_S ? IQ2_1024_MAXCH : IQ2_512_MAXCH;
     __shared__ uint8_t cmap[64 * MAXCH];
     __shared__ unsigned long long res[64];
-    for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
+    stage_levels<2, 8, GS>(T.grid, glds);
     const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
@@ -543,12 +578,12 @@ template <int SRC, bool IS_S, bool IMAT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
     constexpr int LPS = 8, SPW = 8, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
     __shared__ IqLds<SPW, BYTES> s;
-    __shared__ uint16_t glds[GS];
+    __shared__ __align__(16) uint32_t glds[GS];
     __shared__ int act_lds[SPW][8];
     constexpr int MAXCH = IS_S ? IQ3_512_MAXCH : IQ3_256_MAXCH;
     __shared__ uint8_t cmap[64 * MAXCH];
     __shared__ unsigned long long res[64];
-    for (int i = threadIdx.x; i < GS; i += 64) glds[i] = T.grid[i];
+    stage_levels<3, 4, GS>(T.grid, glds);
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
