@@ -43,46 +43,52 @@ __global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
     const int q = tid & 3;                       // quarter of the block: values 8q..8q+7
     const int64_t b0 = (int64_t)blockIdx.x * Q40_BLOCKS_PER_WG;
     float x[Q40_TILES][8];
-    // issue every tile's 16-byte loads first: 16 KB of bf16 in flight per workgroup
+    // issue every tile's 16-byte loads first: 16 KB of bf16 in flight per workgroup.
+    // Rows stored back to back (the usual case) index the source flat; only
+    // padded rows pay for the 64-bit division into row and column.
+    const bool flat = a.stride == a.units_per_row * 32;
 #pragma unroll
     for (int u = 0; u < Q40_TILES; u++) {
         int64_t b = b0 + u * Q40_TILE + (tid >> 2);
         b = b < a.n_units ? b : a.n_units - 1;
-        const int64_t row = b / a.units_per_row;
-        const int64_t col = (b % a.units_per_row) * 32 + 8 * q;
-        load_elems<SRC, true, 8>(a.src, row * a.stride + col, x[u]);
+        int64_t e;
+        if (flat) {
+            e = b * 32 + 8 * q;
+        } else {
+            const int64_t row = b / a.units_per_row;
+            e = row * a.stride + (b - row * a.units_per_row) * 32 + 8 * q;
+        }
+        load_elems<SRC, true, 8>(a.src, e, x[u]);
     }
 #pragma unroll
     for (int u = 0; u < Q40_TILES; u++) {
-        // signed value of the largest |x|, first index wins (argmax of abs)
-        float am = fabsf(x[u][0]), mv = x[u][0];
-        int idx = 8 * q;
+        // signed value of the largest |x|, first index wins (argmax of abs):
+        // the lane's max |x|, then its first value of that magnitude, then
+        // the lowest quarter holding the block's max
+        float am = fabsf(x[u][0]);
 #pragma unroll
-        for (int i = 1; i < 8; i++) {
-            const float v = fabsf(x[u][i]);
-            const bool gt = v > am;
-            am = gt ? v : am;
-            mv = gt ? x[u][i] : mv;
-            idx = gt ? 8 * q + i : idx;
-        }
+        for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[u][i]));
+        float mv = x[u][7];
+#pragma unroll
+        for (int i = 6; i >= 0; i--) mv = fabsf(x[u][i]) == am ? x[u][i] : mv;
 #pragma unroll
         for (int m = 1; m <= 2; m <<= 1) {
             const float pam = __shfl_xor(am, m, 4);
             const float pmv = __shfl_xor(mv, m, 4);
-            const int pidx = __shfl_xor(idx, m, 4);
-            const bool take = pam > am || (pam == am && pidx < idx);
+            const bool take = pam > am || (pam == am && (q ^ m) < q);
             am = take ? pam : am;
             mv = take ? pmv : mv;
-            idx = take ? pidx : idx;
         }
-        const float d = mv / -8.0f;
+        const float d = mv * -0.125f;             // == mv / -8.0f: exact scaling by a power of two
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t nib = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             float t = x[u][i] * id;
             t = t + 8.5f;
-            const uint32_t qv = (uint32_t)clampf(floorf(t), 0.0f, 15.0f);
+            // clamp(floor(t), 0, 15) == trunc(clamp(t, 0, 15.5)): truncation is
+            // floor on [0, 15.5] (NaN clamps to 0 either way)
+            const uint32_t qv = (uint32_t)clampf(t, 0.0f, 15.5f);
             nib |= qv << (4 * i);
         }
         // qs[j] = q[j] | q[j+16] << 4: quarters 0/1 take the high nibbles of 2/3
