@@ -56,15 +56,40 @@ def make_inputs(torch, dev, seed: int = 0):
     return xs, qws, host
 
 
-def profiled_traffic() -> int | None:
-    """HBM bytes per launch of the headline kernel, from the rocprofv3 FETCH_SIZE /
-    WRITE_SIZE runs summarised in profiles/ (scaled by a copy of known size)."""
+def profiled(key: str) -> int | None:
+    """A per-launch figure of the headline kernel from the rocprofv3 counter runs
+    summarised in profiles/: HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled by a copy
+    of known size) or VALU wave instructions (SQ_INSTS_VALU)."""
     f = ROOT / "profiles" / "counters_q4_k_imat_9728x2560.md"
     if f.exists():
         for ln in f.read_text().splitlines():
-            if ln.startswith("traffic_bytes_per_launch:"):
+            if ln.startswith(key + ":"):
                 return int(ln.split(":")[1])
     return None
+
+
+def valu_peak(torch, dev, launches: int = 5) -> float:
+    """Measured VALU issue rate (wave instructions per second) of a kernel that
+    issues only independent f32 multiplies and adds (libqs_calib.so)."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "quant-studio_amd" / "_build" / "libqs_calib.so"))
+    lib.qs_calib_valu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.qs_calib_valu_insts.restype = ctypes.c_double
+    lib.qs_calib_valu_insts.argtypes = [ctypes.c_int, ctypes.c_int]
+    grid, iters = 8192, 4096       # ~7 ms per launch
+    out = torch.empty(1, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream()
+    run = lambda: lib.qs_calib_valu(grid, iters, ctypes.c_void_p(out.data_ptr()),
+                                    ctypes.c_void_p(stream.cuda_stream))
+    assert run() == 0
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(launches):
+        run()
+    b.record(stream)
+    torch.cuda.synchronize()
+    sec = a.elapsed_time(b) * 1e-3 / launches
+    return lib.qs_calib_valu_insts(grid, iters) / sec
 
 
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
@@ -136,6 +161,28 @@ def cpu_baseline(oracle, host, qws):
     return {"value": round(2 * n / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"full workload: Q4_K+imatrix on bf16 {SHAPES[0][0]}x{SHAPES[0][1]} and "
                       f"{SHAPES[1][0]}x{SHAPES[1][1]} ({n} values), {dt:.2f} s, one pass"}
+
+
+def q4_0_large(torch, qs, dev, steps: int) -> dict:
+    """Q4_0 on a token_embd-shaped bf16 tensor (151936 x 2560, 778 MB), two
+    rotating copies: the HBM-bound case at a size where launch ramp-up is small."""
+    rows, k = 151936, 2560
+    g = torch.Generator(device=dev).manual_seed(1)
+    xs = [(torch.randn(rows, k, device=dev, generator=g) * 0.01).to(torch.bfloat16) for _ in range(2)]
+    out = torch.empty((rows, k // 32 * 18), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+    for i in range(2):
+        qs.quantize(2, xs[i], None, out=out)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(steps):
+        qs.quantize(2, xs[i % 2], None, out=out)
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    alg = algorithmic_bytes("q4_0", rows * k, k) - 4 * k
+    return {"input_GBps": round(2 * rows * k / (ms * 1e-3) / 1e9, 1), "kernel_ms": round(ms, 4),
+            "hbm_GBps": round(alg / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def copy_peak(torch, dev, steps: int, warmup: int) -> int:
@@ -263,6 +310,8 @@ def main() -> int:
     ap.add_argument("--e2e", default=None,
                     help="run the CLI end to end on a synthetic 4B-class model for these "
                          "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M') and print its own JSON line")
+    ap.add_argument("--valu-peak", action="store_true",
+                    help="time the VALU issue-rate kernel only (the reference for SQ_INSTS_VALU)")
     ap.add_argument("--copy-only", action="store_true",
                     help="time a plain 1 GiB device copy instead (HBM copy peak, and the "
                          "reference size for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counts)")
@@ -279,6 +328,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.copy_only:
         return copy_peak(torch, dev, args.steps, args.warmup)
+    if args.valu_peak:
+        print(json.dumps({"valu_wave_instr_per_s": round(valu_peak(torch, dev, args.steps))}), flush=True)
+        return 0
     if args.e2e:
         return run_e2e(torch, dev, [x.strip() for x in args.e2e.split(";") if x.strip()])
     xs, qws, host = make_inputs(torch, dev)
@@ -318,6 +370,11 @@ def main() -> int:
                                                                host, qws), 3),
             }
 
+    if "q4_0" in sel:
+        per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, max(3, args.steps // 4))
+    peak_valu = valu_peak(torch, dev)
+    insts = profiled("valu_insts_per_launch")
+
     line = {
         "metric": "input GB/s (bf16) per quant type at 1 GPU + % identical blocks vs reference",
         "value": round(value, 3),
@@ -336,9 +393,17 @@ def main() -> int:
                    "parallelism": "1 GPU (no exchange)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                     "traffic": profiled_traffic(),
+                     "traffic": profiled("traffic_bytes_per_launch"),
                      "kernel": "k_q45_k<bf16, imatrix, 15>", "kernel_ms": round(kms[0], 4),
-                     "algorithmic_bytes": alg},
+                     "algorithmic_bytes": alg,
+                     # the kernel is VALU-bound: its SQ_INSTS_VALU per launch over its
+                     # live duration, against the measured issue rate of a pure
+                     # mul/add kernel
+                     "valu": None if insts is None else {
+                         "insts_per_launch": insts, "unit": "G wave-instr/s",
+                         "achieved": round(insts / (kms[0] * 1e-3) / 1e9, 1),
+                         "peak": round(peak_valu / 1e9, 1),
+                         "frac": round(insts / (kms[0] * 1e-3) / peak_valu, 4)}},
         "per_type": per_type,
     }
     if not args.no_cpu:

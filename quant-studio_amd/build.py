@@ -19,6 +19,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "_build" / "libqs_hip.so"
+CALIB_OUT = PKG / "_build" / "libqs_calib.so"       # measurement aid for bench.py
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -31,10 +32,16 @@ SOURCES = ["qs_api.hip", "qs_pipeline.cpp"]
 
 
 def build(verbose: bool = False) -> Path:
-    OUT.parent.mkdir(parents=True, exist_ok=True)
-    tmp = OUT.with_name(OUT.name + ".tmp")
+    _compile(OUT, SOURCES, verbose)
+    _compile(CALIB_OUT, ["qs_calib.hip"], verbose)
+    return OUT
+
+
+def _compile(out: Path, sources: list[str], verbose: bool) -> None:
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_name(out.name + ".tmp")
     cmd = [HIPCC, *FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", "-o", str(tmp),
-           *[str(CSRC / s) for s in SOURCES]]
+           *[str(CSRC / s) for s in sources]]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -45,8 +52,7 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({r.returncode})")
     if noise and verbose:
         sys.stderr.write("\n".join(noise) + "\n")
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":
