@@ -53,6 +53,10 @@ def lib() -> ctypes.CDLL:
         L.qso_f32_to_f16.argtypes = [ctypes.c_float]
         L.qso_set_sqrt_hook.restype = None
         L.qso_set_sqrt_hook.argtypes = [ctypes.c_void_p]
+        L.qso_set_sqrt_ieee.restype = None
+        L.qso_set_sqrt_ieee.argtypes = [ctypes.c_int]
+        L.qso_sqrt_ref.restype = ctypes.c_float
+        L.qso_sqrt_ref.argtypes = [ctypes.c_float]
         L.qso_set_mutation.restype = None
         L.qso_set_mutation.argtypes = [ctypes.c_int]
         _lib = L
@@ -92,9 +96,20 @@ SQRT_FN = ctypes.CFUNCTYPE(ctypes.c_float, ctypes.c_float)
 _hook_ref = None
 
 
+def sqrt_ref(v: float) -> np.float32:
+    """The oracle's square root: IEEE sqrtf minus one ulp on the tabulated set
+    where the reference's torch.sqrt (CPU) rounds down."""
+    return np.float32(lib().qso_sqrt_ref(float(v)))
+
+
+def use_ieee_sqrt(enable: bool) -> None:
+    """Make the oracle use plain IEEE sqrtf for its weights (tests only)."""
+    lib().qso_set_sqrt_ieee(1 if enable else 0)
+
+
 def use_torch_sqrt(enable: bool) -> None:
-    """Make the oracle take its square roots from torch's CPU sqrt (the routine
-    the reference's eager path calls) instead of IEEE sqrtf. Single-threaded
+    """Make the oracle call torch's CPU sqrt live (the routine the reference's
+    eager path calls) instead of its tabulated reproduction. Single-threaded
     use only (the callback takes the GIL)."""
     global _hook_ref
     if enable:

@@ -40,13 +40,56 @@ static inline float RDIV(float c, float t) {
 }
 static inline float RINT(float v) { return g_mut == MUT_ROUND_AWAY ? roundf(v) : rintf(v); }
 
-/* Square root: IEEE sqrtf by default. The reference's torch.sqrt on CPU is a
- * library routine that is not correctly rounded (about 0.6% of results are one
- * ulp low); a test can install that routine here to reproduce the reference's
- * weights exactly. */
+/* Square root of the reference: torch.sqrt on a CPU tensor (MKL's vectorised
+ * routine), which returns the float just below the IEEE root for 0.59% of
+ * inputs, a set that depends only on the mantissa and the exponent's parity
+ * (qs_sqrt_table.h, generated from torch.sqrt itself). sqrt_ref = IEEE sqrtf,
+ * minus one ulp on that set. A test can install another routine (e.g. torch's,
+ * called live) with qso_set_sqrt_hook, or plain IEEE sqrtf with
+ * qso_set_sqrt_ieee. */
+#include "../quant-studio_amd/csrc/qs_sqrt_table.h"
+
+static uint32_t g_sqrt_down[1 << 19];     /* 2^24-bit map, built once */
+static int g_sqrt_ready = 0;
+static void sqrt_table_init(void) {
+    if (g_sqrt_ready) return;
+    uint32_t key = 0;
+    for (int i = 0; i < QS_SQRT_DOWN_N; i++) {
+        key += QS_SQRT_DOWN_GAPS[i];
+        g_sqrt_down[key >> 5] |= 1u << (key & 31);
+    }
+    g_sqrt_ready = 1;
+}
+
+float qso_sqrt_ref(float v) {
+    sqrt_table_init();
+    float r = sqrtf(v);
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    if (b - 1u < 0x7f7fffffu) {                      /* 0 < v < inf */
+        if (b < 0x00800000u) {                        /* subnormal: scale by 2^64 (exact) */
+            float n = v * 18446744073709551616.0f;
+            memcpy(&b, &n, 4);
+        }
+        uint32_t key = ((((b >> 23) & 1u) ^ 1u) << 23) | (b & 0x7fffffu);
+        if ((g_sqrt_down[key >> 5] >> (key & 31)) & 1u) {
+            uint32_t rb;
+            memcpy(&rb, &r, 4);
+            rb -= 1u;
+            memcpy(&r, &rb, 4);
+        }
+    }
+    return r;
+}
+
 static float (*g_sqrt_hook)(float) = 0;
+static int g_sqrt_ieee = 0;
 void qso_set_sqrt_hook(float (*fn)(float)) { g_sqrt_hook = fn; }
-static inline float SQRT(float v) { return g_sqrt_hook ? g_sqrt_hook(v) : sqrtf(v); }
+void qso_set_sqrt_ieee(int on) { g_sqrt_ieee = on; }
+static inline float SQRT(float v) {
+    if (g_sqrt_hook) return g_sqrt_hook(v);
+    return g_sqrt_ieee ? sqrtf(v) : qso_sqrt_ref(v);
+}
 static inline float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
 /* ------------------------------------------------------------------ */
@@ -789,6 +832,7 @@ int qso_quantize(int type, const float *x, int64_t n_rows, int64_t k, const floa
     int64_t nb = k / blk, total = n_rows * nb;
     int bad = 0;
     if (n_threads < 1) n_threads = 1;
+    sqrt_table_init();                   /* before the worker threads read it */
 #pragma omp parallel for schedule(dynamic, 64) num_threads(n_threads) reduction(| : bad)
     for (int64_t b = 0; b < total; b++) {
         int64_t r = b / nb, c = b % nb;

@@ -41,8 +41,12 @@ float qso_sum_tree(const float *v, int n);
 uint16_t qso_f32_to_f16(float f);
 /* Test hook: plant a known mistake (1..6, see qs_oracle.c); 0 restores the oracle. */
 void qso_set_mutation(int m);
-/* Test hook: square root used for weights (NULL = IEEE sqrtf). */
+/* Square root used for weights: by default the reference's torch.sqrt,
+ * reproduced as IEEE sqrtf minus one ulp on a tabulated set (qso_sqrt_ref).
+ * Test hooks: another routine (NULL = the default), or plain IEEE sqrtf. */
+float qso_sqrt_ref(float v);
 void qso_set_sqrt_hook(float (*fn)(float));
+void qso_set_sqrt_ieee(int on);
 /* Neighbour list of an off-grid code (tables 0..4: IQ2 256/512/1024, IQ3 256/512):
  * writes up to cap grid indices, returns the list length (0 for on-grid codes). */
 int qso_neighbours(int which, int code, uint16_t *out, int cap);

@@ -18,6 +18,7 @@
 #include "qs_host.h"
 #include "qs_iq.h"
 #include "qs_kernels.h"
+#include "qs_sqrt_table.h"
 
 namespace {
 thread_local std::string g_err;
@@ -153,7 +154,26 @@ const HostTab& host_tab(int id) {
 }
 
 std::mutex g_dev_mutex;
-std::map<int, std::array<qs::IqTabDev, IQT_N>> g_dev_tabs;
+// Per-device constant tables: the IQ grids and neighbour lists, and the
+// square-root map of sqrt_ref (2^24 bits expanded from qs_sqrt_table.h).
+struct DevTables {
+    std::array<qs::IqTabDev, IQT_N> iq{};
+    const uint32_t* sqrt_down = nullptr;
+};
+
+const std::vector<uint32_t>& sqrt_down_bits() {
+    static std::once_flag once;
+    static std::vector<uint32_t> bits;
+    std::call_once(once, [] {
+        bits.assign(1u << 19, 0u);
+        uint32_t key = 0;
+        for (int i = 0; i < QS_SQRT_DOWN_N; i++) {
+            key += QS_SQRT_DOWN_GAPS[i];
+            bits[key >> 5] |= 1u << (key & 31u);
+        }
+    });
+    return bits;
+}
 
 template <typename T>
 const T* upload(const std::vector<T>& v) {
@@ -165,26 +185,36 @@ const T* upload(const std::vector<T>& v) {
     return static_cast<const T*>(p);
 }
 
-// Device tables of the current device (uploaded on its first IQ call; kept
-// until the process ends).
-bool device_tabs(std::array<qs::IqTabDev, IQT_N>& out) {
+// Tables of the current device, uploaded on first use (the IQ tables only
+// when an IQ type asks for them) and kept until the process ends.
+struct DevState {
+    DevTables t;
+    bool iq_ready = false;
+};
+std::map<int, DevState> g_dev_state;
+
+bool device_tables(bool need_iq, DevTables& out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     std::lock_guard<std::mutex> lock(g_dev_mutex);
-    auto it = g_dev_tabs.find(dev);
-    if (it == g_dev_tabs.end()) {
-        std::array<qs::IqTabDev, IQT_N> d{};
+    DevState& d = g_dev_state[dev];
+    if (!d.t.sqrt_down) {
+        d.t.sqrt_down = upload(sqrt_down_bits());
+        if (!d.t.sqrt_down) return false;
+    }
+    if (need_iq && !d.iq_ready) {
         for (int id = 0; id < IQT_N; id++) {
             const HostTab& h = host_tab(id);
-            d[id].grid = upload(h.grid);
-            d[id].cinfo = upload(h.cinfo);
-            d[id].nbr = upload(h.nbr);
-            d[id].code0 = h.code0;
-            if (!h.ok || !d[id].grid || !d[id].cinfo || !d[id].nbr) return false;
+            qs::IqTabDev& g = d.t.iq[id];
+            g.grid = upload(h.grid);
+            g.cinfo = upload(h.cinfo);
+            g.nbr = upload(h.nbr);
+            g.code0 = h.code0;
+            if (!h.ok || !g.grid || !g.cinfo || !g.nbr) return false;
         }
-        it = g_dev_tabs.emplace(dev, d).first;
+        d.iq_ready = true;
     }
-    out = it->second;
+    out = d.t;
     return true;
 }
 
@@ -375,17 +405,17 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     a.qw = imat ? imatrix : nullptr;
     a.dst = static_cast<uint8_t*>(dst);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    std::array<qs::IqTabDev, IQT_N> tabs{};
-    if (t->blk == 256 && (ggml_type == QS_TYPE_IQ2_XXS || ggml_type == QS_TYPE_IQ2_XS ||
-                          ggml_type == QS_TYPE_IQ2_S || ggml_type == QS_TYPE_IQ3_XXS ||
-                          ggml_type == QS_TYPE_IQ3_S)) {
-        if (!device_tabs(tabs)) return fail(QS_EIO, "%s: cannot upload grid tables to the device", t->name);
-    }
+    const bool need_iq = ggml_type == QS_TYPE_IQ2_XXS || ggml_type == QS_TYPE_IQ2_XS ||
+                         ggml_type == QS_TYPE_IQ2_S || ggml_type == QS_TYPE_IQ3_XXS || ggml_type == QS_TYPE_IQ3_S;
+    DevTables tabs;
+    if (!device_tables(need_iq, tabs))
+        return fail(QS_EIO, "%s: cannot upload constant tables to the device", t->name);
+    a.sqrt_down = tabs.sqrt_down;
     (void)hipGetLastError();
     switch (src_type) {
-    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs); break;
-    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs); break;
-    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs); break;
+    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs.iq); break;
+    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs.iq); break;
+    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs.iq); break;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(QS_EIO, "%s: launch failed: %s", t->name, hipGetErrorString(e));

@@ -8,7 +8,9 @@
 //     divide-sqrt, hipcc's default);
 //   - torch's `python_float / tensor` is `tensor.reciprocal() * float`
 //     (two roundings), which rdiv() restates;
-//   - torch.round is round-half-even: rintf -> v_rndne_f32.
+//   - torch.round is round-half-even: rintf -> v_rndne_f32;
+//   - torch.sqrt on a CPU tensor is not correctly rounded: sqrt_ref() is the
+//     IEEE root minus one ulp on the tabulated set where torch rounds down.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,6 +24,16 @@ constexpr int QK_K = 256;
 constexpr float GROUP_MAX_EPS = 1e-15f;
 constexpr float F32_TINY = 1.17549435e-38f;
 
+// native 4 x u32 vector (nontemporal loads need a builtin vector type)
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte load: the source is read exactly once, so it is fetched
+// non-temporally and does not push the kernels' constant tables (imatrix,
+// square-root map, IQ lists) out of L2.
+QS_DEV u32x4 load_stream16(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 // source element encodings (ggml type ids)
 enum : int { SRC_F32 = 0, SRC_F16 = 1, SRC_BF16 = 30 };
 
@@ -30,6 +42,58 @@ QS_DEV float rdiv(float c, float t) {
     return r * c;
 }
 QS_DEV float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
+
+// The reference's square root (torch.sqrt on CPU, kernels/q4_k.py:34, :51,
+// iq2.py:431, :436 and the other weight sites): the IEEE root, one ulp lower
+// when the input's key (exponent parity << 23 | mantissa, subnormals scaled
+// by 2^64 first) is set in `down`, a 2^24-bit map built per device from
+// qs_sqrt_table.h. Zero, negative, infinite and NaN inputs keep the IEEE result.
+QS_DEV uint32_t sqrt_key(float v) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t bn = b < 0x00800000u ? __float_as_uint(v * 18446744073709551616.0f) : b;
+    return ((((bn >> 23) & 1u) ^ 1u) << 23) | (bn & 0x7fffffu);     // always < 2^24
+}
+
+QS_DEV float sqrt_fix(float v, uint32_t key, uint32_t word) {
+    const float r = sqrtf(v);
+    const bool dn = (__float_as_uint(v) - 1u < 0x7f7fffffu) && ((word >> (key & 31u)) & 1u);
+    return dn ? __uint_as_float(__float_as_uint(r) - 1u) : r;
+}
+
+QS_DEV float sqrt_ref(float v, const uint32_t* __restrict__ down) {
+    const uint32_t key = sqrt_key(v);
+    return sqrt_fix(v, key, down[key >> 5]);
+}
+
+// sqrt_ref over a lane's N values, every map load issued before any is used
+template <int N>
+QS_DEV void sqrt_ref_n(const float (&v)[N], const uint32_t* __restrict__ down, float (&out)[N]) {
+    uint32_t key[N], word[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) key[i] = sqrt_key(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; i++) word[i] = down[key[i] >> 5];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = sqrt_fix(v[i], key[i], word[i]);
+}
+
+// imatrix weights w[i] = qw[i] * sqrt_ref(sigma2 + x[i]^2) (e.g. q4_k.py:51),
+// with the imatrix and map loads issued together
+template <int N>
+QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const float (&x)[N],
+                            const uint32_t* __restrict__ down, float (&w)[N]) {
+    float v[N], q[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float t = x[i] * x[i];
+        v[i] = sigma2 + t;
+        q[i] = qw[i];
+    }
+    float r[N];
+    sqrt_ref_n<N>(v, down, r);
+#pragma unroll
+    for (int i = 0; i < N; i++) w[i] = q[i] * r[i];
+}
 
 // f32 -> fp16 bits, round to nearest even (v_cvt_f16_f32 under the default mode)
 QS_DEV uint32_t f16_bits(float v) {
@@ -47,7 +111,7 @@ QS_DEV void load_elems(const void* base, int64_t off, float (&out)[N]) {
         if constexpr (VEC) {
 #pragma unroll
             for (int j = 0; j < N / 8; j++) {
-                uint4 u = reinterpret_cast<const uint4*>(p)[j];
+                const u32x4 u = load_stream16(p + 8 * j);
                 uint32_t v[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -64,7 +128,7 @@ QS_DEV void load_elems(const void* base, int64_t off, float (&out)[N]) {
         if constexpr (VEC) {
 #pragma unroll
             for (int j = 0; j < N / 8; j++) {
-                uint4 u = reinterpret_cast<const uint4*>(p)[j];
+                const u32x4 u = load_stream16(p + 8 * j);
                 uint32_t v[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
@@ -81,11 +145,13 @@ QS_DEV void load_elems(const void* base, int64_t off, float (&out)[N]) {
         if constexpr (VEC) {
 #pragma unroll
             for (int j = 0; j < N / 4; j++) {
-                float4 u = reinterpret_cast<const float4*>(p)[j];
-                out[4 * j] = u.x;
-                out[4 * j + 1] = u.y;
-                out[4 * j + 2] = u.z;
-                out[4 * j + 3] = u.w;
+                const u32x4 u = load_stream16(p + 4 * j);
+                // copy the lanes out before reinterpreting them: hipcc narrows
+                // the load to one dword when __builtin_bit_cast is applied to
+                // an ext_vector element directly
+                const uint32_t v[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int t = 0; t < 4; t++) out[4 * j + t] = __builtin_bit_cast(float, v[t]);
             }
         } else {
 #pragma unroll

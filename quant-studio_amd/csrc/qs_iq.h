@@ -335,11 +335,7 @@ QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float* vlds, float* 
     wave_sync();
     const float sum = sb_cascade8_256<LPS>(vlds, tmp, p.g);
     const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
-#pragma unroll
-    for (int i = 0; i < GROUP; i++) {
-        const float t = x[i] * x[i];
-        w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
-    }
+    imatrix_weights<GROUP>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
 }
 
 // ------------------------------------------------------------------
@@ -357,8 +353,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
     iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 1.0f, false, x, w);
-#pragma unroll
-    for (int i = 0; i < 32; i++) waux[i] = sqrtf(w[i]);
+    sqrt_ref_n<32>(w, a.sqrt_down, waux);
     int signs[4];
     static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
     float gmax = xval[0];
@@ -461,8 +456,7 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
     iq_load_weights<SRC, LPS, 16>(a, p, s.v[slot], s.tmp[slot], IS_S ? 2.0f : 1.0f, false, x, w);
-#pragma unroll
-    for (int i = 0; i < 16; i++) waux[i] = sqrtf(w[i]);
+    sqrt_ref_n<16>(w, a.sqrt_down, waux);
     int signs[2];
     if constexpr (IS_S) {
         signs[0] = sign_bits8<0>(x, xval);
@@ -588,8 +582,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
     iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 2.0f, !IMAT, x, w);
-#pragma unroll
-    for (int i = 0; i < 32; i++) waux[i] = sqrtf(w[i]);
+    sqrt_ref_n<32>(w, a.sqrt_down, waux);
     int signs[4];
     if constexpr (IS_S) {
         static_for<0, 4>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });

@@ -23,6 +23,7 @@ struct KArgs {
     int64_t stride;       // source row stride in elements
     const float* qw;      // k imatrix weights or nullptr
     uint8_t* dst;         // packed output, n_units * block bytes
+    const uint32_t* sqrt_down;   // sqrt_ref's 2^24-bit map (device copy)
 };
 
 struct QpSteps {
@@ -161,7 +162,7 @@ QS_DEV void sb_store(const SbLds<SPW, BYTES>& s, const KArgs& a) {
 // Q4_K / Q5_K  (q4_k.py:25-79, q5_k.py:25-82)
 // ------------------------------------------------------------------
 template <int SRC, bool IMAT, int NMAX>
-__global__ __launch_bounds__(64) void k_q45_k(KArgs a, Steps steps, QpSteps qps) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_q45_k(KArgs a, Steps steps, QpSteps qps) {
     constexpr int LPS = 8, SPW = 8, BYTES = NMAX == 15 ? 144 : 176;
     constexpr float FMAX = (float)NMAX;
     __shared__ SbLds<SPW, BYTES> s;
@@ -176,16 +177,12 @@ __global__ __launch_bounds__(64) void k_q45_k(KArgs a, Steps steps, QpSteps qps)
         wave_sync();
         const float sum = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g);
         const float sigma2 = (2.0f * sum) / 256.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const float t = x[i] * x[i];
-            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
-        }
+        imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
     } else {
         float t[32];
 #pragma unroll
         for (int i = 0; i < 32; i++) t[i] = x[i] * x[i];
-        const float av = sqrtf(cascade8_sum(t) / 32.0f);
+        const float av = sqrt_ref(cascade8_sum(t) / 32.0f, a.sqrt_down);
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = av + fabsf(x[i]);
     }
@@ -387,11 +384,7 @@ __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps3
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = (2.0f * sb_seq_256(s.v[slot])) / 256.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float t = x[i] * x[i];
-            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
-        }
+        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
         const QxResult r = qx_fit<16>(x, w, 4, steps4);
 #pragma unroll
         for (int i = 0; i < 16; i++) Lg[i] = qx_level(r, x[i], 4.0f);
@@ -499,11 +492,7 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g) / 256.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float t = x[i] * x[i];
-            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
-        }
+        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
         r = qkx_fit<16, false>(x, w, steps, 3.0f);
         s.sc[slot][g] = r.scale;
         s.mn[slot][g] = r.the_min;
@@ -576,7 +565,7 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
 // IQ4_XS  (iq4_xs.py:149-188)
 // ------------------------------------------------------------------
 template <int SRC, bool IMAT>
-__global__ __launch_bounds__(64) void k_iq4_xs(KArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_xs(KArgs a) {
     constexpr int LPS = 8, SPW = 8, BYTES = 136;
     __shared__ SbLds<SPW, BYTES> s;
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
@@ -588,11 +577,7 @@ __global__ __launch_bounds__(64) void k_iq4_xs(KArgs a) {
         for (int i = 0; i < 32; i++) s.v[slot][32 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = (2.0f * sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g)) / 256.0f;
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const float t = x[i] * x[i];
-            w[i] = a.qw[p.col + i] * sqrtf(sigma2 + t);
-        }
+        imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];

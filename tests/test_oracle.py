@@ -22,36 +22,63 @@ from golden_data import ORACLE_TYPES, block_identical, cases
 
 @pytest.mark.parametrize("qtype", ORACLE_TYPES)
 def test_oracle_matches_reference_golden(qtype):
-    """With torch's CPU square root installed (the routine the reference calls),
-    the oracle reproduces every golden block of every type."""
+    """The oracle (with its tabulated reproduction of torch's CPU square root)
+    reproduces every golden block of every type."""
+    for key, x, qw, expect in cases(qtype):
+        got = oracle.quantize(qtype, x, qw, n_threads=4)
+        same = block_identical(got, expect, qtype)
+        assert same.all(), f"{qtype} {key}: {int((~same).sum())} of {same.size} blocks differ"
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "iq2_s", "iq3_xxs"])
+def test_tabulated_sqrt_equals_live_torch_sqrt_in_the_oracle(qtype):
+    """Calling torch.sqrt live from the oracle gives the same bytes as the table."""
+    key, x, qw, expect = cases(qtype)[0]
+    base = oracle.quantize(qtype, x, qw, n_threads=1)
     oracle.use_torch_sqrt(True)
     try:
-        for key, x, qw, expect in cases(qtype):
-            got = oracle.quantize(qtype, x, qw, n_threads=1)
-            same = block_identical(got, expect, qtype)
-            assert same.all(), f"{qtype} {key}: {int((~same).sum())} of {same.size} blocks differ"
+        live = oracle.quantize(qtype, x, qw, n_threads=1)
     finally:
         oracle.use_torch_sqrt(False)
+    assert np.array_equal(base, live)
 
 
-@pytest.mark.parametrize("qtype", ORACLE_TYPES)
-def test_oracle_ieee_sqrt_vs_reference_golden(qtype):
-    """With IEEE sqrtf (what the GPU kernels use) the golden blocks still match
-    except where torch's not-correctly-rounded sqrt decides an exact tie."""
-    same = total = 0
-    for key, x, qw, expect in cases(qtype):
-        s = block_identical(oracle.quantize(qtype, x, qw, n_threads=4), expect, qtype)
-        same += int(s.sum())
-        total += s.size
-    assert same / total >= 0.995, f"{qtype}: {total - same} of {total} blocks differ"
+def test_tabulated_sqrt_matches_torch_on_random_inputs():
+    """qso_sqrt_ref == torch.sqrt (CPU) bit for bit: random positive normals and
+    subnormals, powers of 4 apart, and the special values."""
+    rng = np.random.default_rng(11)
+    bits = np.concatenate([rng.integers(0x00800000, 0x7f800000, 200_000, dtype=np.uint32),
+                           rng.integers(1, 0x00800000, 20_000, dtype=np.uint32)])
+    x = bits.view(np.float32)
+    x = np.concatenate([x, x[:1000] * np.float32(4.0), x[:1000] * np.float32(0.25),
+                        np.array([0.0, -0.0, np.inf, -1.0, np.nan], np.float32)])
+    want = torch.sqrt(torch.from_numpy(x)).numpy()
+    got = np.array([oracle.sqrt_ref(v) for v in x], np.float32)
+    assert np.array_equal(got.view(np.uint32)[:-2], want.view(np.uint32)[:-2])
+    assert np.isnan(got[-2]) and np.isnan(got[-1])
+
+
+@pytest.mark.parametrize("qtype", ["iq2_s"])
+def test_ieee_sqrt_would_change_a_golden_block(qtype):
+    """Why the table exists: with IEEE sqrtf instead of torch's rounding, one
+    golden IQ2_S block (an exact tie in the sweep's accept test) differs."""
+    oracle.use_ieee_sqrt(True)
+    try:
+        diff = 0
+        for key, x, qw, expect in cases(qtype):
+            diff += int((~block_identical(oracle.quantize(qtype, x, qw, n_threads=4), expect, qtype)).sum())
+    finally:
+        oracle.use_ieee_sqrt(False)
+    assert diff >= 1
 
 
 def test_torch_cpu_sqrt_is_not_correctly_rounded():
-    """The fact the sqrt hook exists for: torch.sqrt on CPU returns one ulp
-    below the correctly rounded root for some inputs."""
+    """torch.sqrt on CPU returns one ulp below the correctly rounded root for
+    some inputs (the set the table holds)."""
     v = np.array([0.019531157], np.float32)
     assert np.sqrt(v)[0] == np.float32(0.13975392)
     assert torch.sqrt(torch.from_numpy(v)).numpy()[0] == np.float32(0.13975391)
+    assert oracle.sqrt_ref(v[0]) == np.float32(0.13975391)
 
 
 @pytest.mark.parametrize("n", [8, 16, 32, 256])
