@@ -301,17 +301,40 @@ QS_DEV int iq4_index(float al) {
     return (al - lo < hi - al) ? mu - 1 : mu;
 }
 
-QS_DEV float iq4_value(int idx) {
+// Bracket table of _best_index (iq4_xs.py:35-39): the LUT values are integers,
+// so #{V <= al} = #{V <= floor(al)}; entry k + 128 (k = -128..127) holds the
+// bracket (V[mu-1], V[mu]) with mu = clamp(#{V <= k}, 1, 15). Built by the
+// workgroup in LDS.
+QS_DEV void iq4_build_table(float2* tab) {
     constexpr float V[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                              1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
-    float v = V[0];
+    for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+        const float k = (float)(e - 128);
+        int mu = 0;
 #pragma unroll
-    for (int i = 1; i < 16; i++) v = (idx == i) ? V[i] : v;
-    return v;
+        for (int i = 0; i < 16; i++) mu += (V[i] <= k) ? 1 : 0;
+        mu = mu < 1 ? 1 : (mu > 15 ? 15 : mu);
+        float lo = V[0], hi = V[1];
+#pragma unroll
+        for (int i = 2; i < 16; i++) {
+            lo = (mu == i) ? V[i - 1] : lo;
+            hi = (mu == i) ? V[i] : hi;
+        }
+        tab[e] = make_float2(lo, hi);
+    }
+}
+
+// LUT value of _best_index(al): the bracket from the table, then the C
+// midpoint compare `al - lo < hi - al` (strict; NaN takes hi, as the scan)
+QS_DEV float iq4_project(float al, const float2* tab) {
+    const float f = clampf(floorf(al), -128.0f, 127.0f);
+    const float2 e = tab[(int)f + 128];
+    const float d1 = al - e.x, d2 = e.y - al;
+    return d1 < d2 ? e.x : e.y;
 }
 
 // _search_scales_eager iq4_xs.py:52-76 for one block of 32
-QS_DEV float iq4_scale_search(const float (&x)[32], const float (&w)[32]) {
+QS_DEV float iq4_scale_search(const float (&x)[32], const float (&w)[32], const float2* tab) {
     float amax;
     const float mx = absmax_first(x, amax);
     const bool live = fabsf(mx) >= GROUP_MAX_EPS;
@@ -321,7 +344,7 @@ QS_DEV float iq4_scale_search(const float (&x)[32], const float (&w)[32]) {
     float t[32], u[32];
 #pragma unroll
     for (int i = 0; i < 32; i++) {
-        float q = iq4_value(iq4_index(id0 * x[i]));
+        float q = iq4_project(id0 * x[i], tab);
         float wq = w[i] * q;
         t[i] = wq * x[i];
         u[i] = wq * q;
@@ -334,7 +357,7 @@ QS_DEV float iq4_scale_search(const float (&x)[32], const float (&w)[32]) {
         const float idv = rdiv((float)(itry - 127), mxs);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
-            float q = iq4_value(iq4_index(idv * x[i]));
+            float q = iq4_project(idv * x[i], tab);
             float wq = w[i] * q;
             t[i] = wq * x[i];
             u[i] = wq * q;

@@ -568,6 +568,8 @@ template <int SRC, bool IMAT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_xs(KArgs a) {
     constexpr int LPS = 8, SPW = 8, BYTES = 136;
     __shared__ SbLds<SPW, BYTES> s;
+    __shared__ float2 iq4tab[256];
+    iq4_build_table(iq4tab);
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32];
@@ -582,7 +584,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
     }
-    const float scale = iq4_scale_search(x, w);
+    if constexpr (!IMAT) wave_sync();          // iq4tab ready (the imatrix path synced above)
+    const float scale = iq4_scale_search(x, w, iq4tab);
     s.sc[slot][g] = scale;
     wave_sync();
     float sc8[8];
