@@ -281,31 +281,11 @@ QS_DEV float q3_fit(const float (&x)[N], int nmax, float (&L)[N]) {
 
 // ---- IQ4_XS (iq4_xs.py:23-76) ----
 
-// best_index_int8 iq4_xs.py:35-39: count LUT entries <= al (searchsorted
-// right), clamp to 1..15, then the strict midpoint compare.
-QS_DEV int iq4_index(float al) {
-    constexpr float V[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
-                             1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
-    int mu = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) mu += (V[i] <= al) ? 1 : 0;
-    mu = mu < 1 ? 1 : (mu > 15 ? 15 : mu);
-    // lo = V[mu-1], hi = V[mu] without dynamic register indexing
-    float lo = V[0], hi = V[1];
-#pragma unroll
-    for (int i = 2; i < 16; i++) {
-        bool sel = (mu == i);
-        lo = sel ? V[i - 1] : lo;
-        hi = sel ? V[i] : hi;
-    }
-    return (al - lo < hi - al) ? mu - 1 : mu;
-}
-
 // Bracket table of _best_index (iq4_xs.py:35-39): the LUT values are integers,
 // so #{V <= al} = #{V <= floor(al)}; entry k + 128 (k = -128..127) holds the
-// bracket (V[mu-1], V[mu]) with mu = clamp(#{V <= k}, 1, 15). Built by the
-// workgroup in LDS.
-QS_DEV void iq4_build_table(float2* tab) {
+// bracket (V[mu-1], V[mu]) with mu = clamp(#{V <= k}, 1, 15), and mu itself in
+// `mus`. Built by the workgroup in LDS.
+QS_DEV void iq4_build_table(float2* tab, uint8_t* mus) {
     constexpr float V[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
                              1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
     for (int e = threadIdx.x; e < 256; e += blockDim.x) {
@@ -321,6 +301,7 @@ QS_DEV void iq4_build_table(float2* tab) {
             hi = (mu == i) ? V[i] : hi;
         }
         tab[e] = make_float2(lo, hi);
+        mus[e] = (uint8_t)mu;
     }
 }
 
@@ -331,6 +312,15 @@ QS_DEV float iq4_project(float al, const float2* tab) {
     const float2 e = tab[(int)f + 128];
     const float d1 = al - e.x, d2 = e.y - al;
     return d1 < d2 ? e.x : e.y;
+}
+
+// LUT index of _best_index(al), from the same table
+QS_DEV int iq4_project_index(float al, const float2* tab, const uint8_t* mus) {
+    const int k = (int)clampf(floorf(al), -128.0f, 127.0f) + 128;
+    const float2 e = tab[k];
+    const int mu = mus[k];
+    const float d1 = al - e.x, d2 = e.y - al;
+    return d1 < d2 ? mu - 1 : mu;
 }
 
 // _search_scales_eager iq4_xs.py:52-76 for one block of 32

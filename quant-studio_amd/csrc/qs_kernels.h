@@ -569,7 +569,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     constexpr int LPS = 8, SPW = 8, BYTES = 136;
     __shared__ SbLds<SPW, BYTES> s;
     __shared__ float2 iq4tab[256];
-    iq4_build_table(iq4tab);
+    __shared__ uint8_t iq4mu[256];
+    iq4_build_table(iq4tab, iq4mu);
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32];
@@ -599,7 +600,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     const float dl = d * lsf;
     const float idl = dl != 0.0f ? 1.0f / dl : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) s.L[slot][32 * g + i] = (uint8_t)iq4_index(idl * x[i]);
+    for (int i = 0; i < 32; i++) s.L[slot][32 * g + i] = (uint8_t)iq4_project_index(idl * x[i], iq4tab, iq4mu);
     s.ls[slot][g] = (int)(lsf + 32.0f);
     if (g == 0) s.hdr[slot][0] = __builtin_bit_cast(float, f16_bits(d));
     wave_sync();
