@@ -150,7 +150,9 @@ QS_DEV int iq_project_wave(const IqTabDev& T, const uint32_t* glds, uint8_t* cma
         if (lane >= d) incl += t;
     }
     const int excl = incl - nch;
-    const int total = __shfl(incl, 63);
+    // the wave's chunk count, held in a scalar register so the round loop is
+    // scalar-controlled
+    const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63));
     for (int i = 0; i < nch; i++) cmap[excl + i] = (uint8_t)lane;
     res[lane] = ~0ull;
     wave_sync();
@@ -180,25 +182,26 @@ QS_DEV int iq_project_wave(const IqTabDev& T, const uint32_t* glds, uint8_t* cma
                 wd[0] = q.x; wd[1] = q.y;
             }
             unsigned long long best = ~0ull;
+            // every slot of the chunk is evaluated (padding holds index 0, a
+            // valid grid point); slots past the list end are masked out of the
+            // minimum, without branches
 #pragma unroll
             for (int j = 0; j < CH; j++) {
                 const int pos = CH * kc + j;
-                if (pos < o_n) {
-                    const int gi = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    const Levels<NV> gl = grid_levels<NV>(glds, gi);
-                    float d2 = 0.0f;
+                const int gi = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                const Levels<NV> gl = grid_levels<NV>(glds, gi);
+                float d2 = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < NV; e++) {
-                        float diff = o_sc * level<NV>(gl, e);
-                        diff = diff - xs[e];
-                        const float t = (ws[e] * diff) * diff;
-                        if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
-                        else d2 = d2 + t;
-                    }
-                    const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
-                                                   ((unsigned long long)pos << 16) | (unsigned)gi;
-                    best = key < best ? key : best;
+                for (int e = 0; e < NV; e++) {
+                    float diff = o_sc * level<NV>(gl, e);
+                    diff = diff - xs[e];
+                    const float t = (ws[e] * diff) * diff;
+                    if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
+                    else d2 = d2 + t;
                 }
+                const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
+                                               ((unsigned long long)pos << 16) | (unsigned)gi;
+                best = (pos < o_n && key < best) ? key : best;
             }
             atomicMin(&res[owner], best);
         }
