@@ -106,10 +106,11 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 }
 
 
-// Project subgroup OFF..OFF+NV-1 of every lane's group at its candidate scale
+// Project every lane's subgroups at its candidate scale
 // (iq2.py:347-372, iq2xs_common.py:222-271, iq3_common.py:209-256): levels
-// clamp(round(0.5*(inv*x - 1)), 0, LMAX) -> code -> kmap hit, or the first
-// minimum of the weighted distance over the code's neighbour list. IQ2
+// clamp(round(0.5*(inv*x - 1)), 0, LMAX) -> code -> kmap hit (iq_codes), or
+// the first minimum of the weighted distance over the code's neighbour list
+// (iq_search, one call per subgroup OFF..OFF+NV-1). IQ2
 // distances are a left-to-right sum of 8 terms from +0; IQ3's are
 // ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and diff = sc*g - x.
 //
@@ -124,22 +125,32 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // nothing (their result is unused).
 //   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
 //   res:  LDS, 64 keys
-template <int BITS, int NV, int OFF, int CH, int MAXCH, int N>
-QS_DEV int iq_project_wave(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, unsigned long long* res,
-                           const float (&xv)[N], const float (&wv)[N], float inv, float sc, bool want,
-                           bool& on) {
-    static_assert(CH == 4 || CH == 8, "chunks are one 8- or 16-byte load");
+template <int BITS, int NV, int NSUB, int N>
+QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB]) {
+    // all subgroups' codes first, so their cinfo loads are in flight together
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
-    const int lane = threadIdx.x;
-    int code = 0;
+    int code[NSUB];
 #pragma unroll
-    for (int j = 0; j < NV; j++) {
-        float t = inv * xv[OFF + j];
-        t = t - 1.0f;
-        t = 0.5f * t;
-        code |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
+    for (int s = 0; s < NSUB; s++) {
+        code[s] = 0;
+#pragma unroll
+        for (int j = 0; j < NV; j++) {
+            float t = inv * xv[NV * s + j];
+            t = t - 1.0f;
+            t = 0.5f * t;
+            code[s] |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
+        }
     }
-    const uint32_t ci = T.cinfo[code];
+#pragma unroll
+    for (int s = 0; s < NSUB; s++) ci[s] = T.cinfo[code[s]];
+}
+
+template <int BITS, int NV, int OFF, int CH, int MAXCH, int N>
+QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, unsigned long long* res,
+                     const float (&xv)[N], const float (&wv)[N], float sc, uint32_t ci, bool want,
+                     bool& on) {
+    static_assert(CH == 4 || CH == 8, "chunks are one 8- or 16-byte load");
+    const int lane = threadIdx.x;
     on = (ci & CI_ON_GRID) != 0;
     const int n = (on || !want) ? 0 : (int)(ci & 0xfffu);
     const int nch = (n + CH - 1) / CH;
@@ -378,8 +389,10 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         const float sc = 1.0f / inv;
         int gi[4];
         bool on;
+        uint32_t ci[4];
+        iq_codes<2, 8, 4>(T, xval, inv, ci);
         static_for<0, 4>([&](auto S) {
-            gi[S] = iq_project_wave<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on);
+            gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
         iq_sums<2, 8, 4>(glds, gi, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
@@ -396,8 +409,10 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         const float inv = 1.0f / (proj ? scale : 1.0f);
         int gp[4];
         bool on;
+        uint32_t ci[4];
+        iq_codes<2, 8, 4>(T, xval, inv, ci);
         static_for<0, 4>([&](auto S) {
-            gp[S] = iq_project_wave<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, inv, scale, proj, on);
+            gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
         iq_sums<2, 8, 4>(glds, gp, w, xval, ta, tb);
         const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
@@ -482,8 +497,10 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         const float inv = rdiv(sweep.v[st], gsafe), sc = 1.0f / inv;
         int gi[2];
         bool on[2];
-        gi[0] = iq_project_wave<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[0]);
-        gi[1] = iq_project_wave<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[1]);
+        uint32_t ci[2];
+        iq_codes<2, 8, 2>(T, xval, inv, ci);
+        gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
+        gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -502,10 +519,12 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
         // lanes that need it are searched and replaced
         const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
-        const int r0 = iq_project_wave<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
-                                                         need && !og[0], on);
-        const int r1 = iq_project_wave<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, scale,
-                                                         need && !og[1], on);
+        uint32_t ci[2];
+        iq_codes<2, 8, 2>(T, xval, inv, ci);
+        const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[0],
+                                                          need && !og[0], on);
+        const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[1],
+                                                          need && !og[1], on);
         if (need && !og[0]) win[0] = r0;
         if (need && !og[1]) win[1] = r1;
     }
@@ -611,8 +630,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
         const float inv = rdiv(steps.v[st], gsafe), sc = 1.0f / inv;
         int gi[8];
         bool on[8];
+        uint32_t ci[8];
+        iq_codes<3, 4, 8>(T, xval, inv, ci);
         static_for<0, 8>([&](auto S) {
-            gi[S] = iq_project_wave<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv, sc, true, on[S]);
+            gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
         float sumqx, sumq2;
         iq_tree_sums<3, 4, 8>(glds, gi, w, xval, sumqx, sumq2);
@@ -635,9 +656,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
         const float inv2 = 1.0f / (redo ? scale : 1.0f);
         int w2[8];
         bool on[8];
+        uint32_t ci[8];
+        iq_codes<3, 4, 8>(T, xval, inv2, ci);
         static_for<0, 8>([&](auto S) {
-            w2[S] = iq_project_wave<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, inv2, scale,
-                                                                redo && (IS_S || !og[S]), on[S]);
+            w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
+                                                          redo && (IS_S || !og[S]), on[S]);
         });
 #pragma unroll
         for (int k = 0; k < 8; k++)
