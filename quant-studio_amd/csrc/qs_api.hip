@@ -118,20 +118,25 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
             p[j] = 2 * l + 1;
         }
         if (!ok) continue;
-        std::vector<int> dist;
+        // the nwant smallest distinct distances (ascending), then every grid
+        // point within the largest of them, in (distance, index) order
+        int small[4];
+        int nd = 0;
         for (int i = 0; i < gs; i++) {
-            int s = 0;
-            for (int j = 0; j < nsub; j++) s += (p[j] - gl[i * nsub + j]) * (p[j] - gl[i * nsub + j]);
-            d2[i] = s;
+            int v = 0;
+            for (int j = 0; j < nsub; j++) v += (p[j] - gl[i * nsub + j]) * (p[j] - gl[i * nsub + j]);
+            d2[i] = v;
+            int pos = 0;
+            while (pos < nd && small[pos] < v) pos++;
+            if ((pos < nd && small[pos] == v) || pos >= nwant) continue;
+            for (int q = std::min(nd, nwant - 1); q > pos; q--) small[q] = small[q - 1];
+            small[pos] = v;
+            nd = std::min(nd + 1, nwant);
         }
-        dist.assign(d2.begin(), d2.end());
-        std::sort(dist.begin(), dist.end());
-        dist.erase(std::unique(dist.begin(), dist.end()), dist.end());
-        const int limit = dist[std::min<int>(nwant, (int)dist.size()) - 1];
         const size_t start = t.nbr.size();     // a multiple of ch: one aligned vector per chunk
-        for (int rank = 0; rank < (int)dist.size() && dist[rank] <= limit; rank++)
+        for (int r = 0; r < nd; r++)
             for (int i = 0; i < gs; i++)
-                if (d2[i] == dist[rank]) t.nbr.push_back((uint16_t)i);
+                if (d2[i] == small[r]) t.nbr.push_back((uint16_t)i);
         const size_t len = t.nbr.size() - start;
         t.nbr.resize((t.nbr.size() + ch - 1) / ch * ch, 0);
         t.cinfo[c] = (uint32_t)((start / ch) << 12) | (uint32_t)len;
@@ -140,17 +145,32 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
     return t;
 }
 
+// one grid's host tables, built on first use of that grid
 const HostTab& host_tab(int id) {
-    static std::once_flag once;
+    static std::array<std::once_flag, IQT_N> once;
     static std::array<HostTab, IQT_N> tabs;
-    std::call_once(once, [] {
-        tabs[IQT_G2_256] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_CH, qs::IQ2_256_MAXCH);
-        tabs[IQT_G2_512] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_CH, qs::IQ2_512_MAXCH);
-        tabs[IQT_G2_1024] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_CH, qs::IQ2_1024_MAXCH);
-        tabs[IQT_G3_256] = build_host_tab(QS_GRID3_256, 256, 3, 2, qs::IQ3_CH, qs::IQ3_256_MAXCH);
-        tabs[IQT_G3_512] = build_host_tab(QS_GRID3_512, 512, 3, 3, qs::IQ3_CH, qs::IQ3_512_MAXCH);
+    std::call_once(once[id], [id] {
+        switch (id) {
+        case IQT_G2_256: tabs[id] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_CH, qs::IQ2_256_MAXCH); break;
+        case IQT_G2_512: tabs[id] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_CH, qs::IQ2_512_MAXCH); break;
+        case IQT_G2_1024: tabs[id] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_CH, qs::IQ2_1024_MAXCH); break;
+        case IQT_G3_256: tabs[id] = build_host_tab(QS_GRID3_256, 256, 3, 2, qs::IQ3_CH, qs::IQ3_256_MAXCH); break;
+        default: tabs[id] = build_host_tab(QS_GRID3_512, 512, 3, 3, qs::IQ3_CH, qs::IQ3_512_MAXCH); break;
+        }
     });
     return tabs[id];
+}
+
+// grid table used by an IQ type (-1 for the other types)
+int iq_table_of(int ggml_type) {
+    switch (ggml_type) {
+    case QS_TYPE_IQ2_XXS: return IQT_G2_256;
+    case QS_TYPE_IQ2_XS: return IQT_G2_512;
+    case QS_TYPE_IQ2_S: return IQT_G2_1024;
+    case QS_TYPE_IQ3_XXS: return IQT_G3_256;
+    case QS_TYPE_IQ3_S: return IQT_G3_512;
+    default: return -1;
+    }
 }
 
 std::mutex g_dev_mutex;
@@ -185,36 +205,30 @@ const T* upload(const std::vector<T>& v) {
     return static_cast<const T*>(p);
 }
 
-// Tables of the current device, uploaded on first use (the IQ tables only
-// when an IQ type asks for them) and kept until the process ends.
-struct DevState {
-    DevTables t;
-    bool iq_ready = false;
-};
-std::map<int, DevState> g_dev_state;
+// Tables of the current device, uploaded on first use (an IQ grid's tables
+// when a type using that grid first runs) and kept until the process ends.
+std::map<int, DevTables> g_dev_state;
 
-bool device_tables(bool need_iq, DevTables& out) {
+bool device_tables(int iq_table, DevTables& out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return false;
     std::lock_guard<std::mutex> lock(g_dev_mutex);
-    DevState& d = g_dev_state[dev];
-    if (!d.t.sqrt_down) {
-        d.t.sqrt_down = upload(sqrt_down_bits());
-        if (!d.t.sqrt_down) return false;
+    DevTables& d = g_dev_state[dev];
+    if (!d.sqrt_down) {
+        d.sqrt_down = upload(sqrt_down_bits());
+        if (!d.sqrt_down) return false;
     }
-    if (need_iq && !d.iq_ready) {
-        for (int id = 0; id < IQT_N; id++) {
-            const HostTab& h = host_tab(id);
-            qs::IqTabDev& g = d.t.iq[id];
-            g.grid = upload(h.grid);
-            g.cinfo = upload(h.cinfo);
-            g.nbr = upload(h.nbr);
-            g.code0 = h.code0;
-            if (!h.ok || !g.grid || !g.cinfo || !g.nbr) return false;
-        }
-        d.iq_ready = true;
+    if (iq_table >= 0 && !d.iq[iq_table].grid) {
+        const HostTab& h = host_tab(iq_table);
+        qs::IqTabDev g{};
+        g.grid = upload(h.grid);
+        g.cinfo = upload(h.cinfo);
+        g.nbr = upload(h.nbr);
+        g.code0 = h.code0;
+        if (!h.ok || !g.grid || !g.cinfo || !g.nbr) return false;
+        d.iq[iq_table] = g;
     }
-    out = d.t;
+    out = d;
     return true;
 }
 
@@ -405,10 +419,8 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     a.qw = imat ? imatrix : nullptr;
     a.dst = static_cast<uint8_t*>(dst);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    const bool need_iq = ggml_type == QS_TYPE_IQ2_XXS || ggml_type == QS_TYPE_IQ2_XS ||
-                         ggml_type == QS_TYPE_IQ2_S || ggml_type == QS_TYPE_IQ3_XXS || ggml_type == QS_TYPE_IQ3_S;
     DevTables tabs;
-    if (!device_tables(need_iq, tabs))
+    if (!device_tables(iq_table_of(ggml_type), tabs))
         return fail(QS_EIO, "%s: cannot upload constant tables to the device", t->name);
     a.sqrt_down = tabs.sqrt_down;
     (void)hipGetLastError();
