@@ -8,8 +8,10 @@
 //     and file write of chunk i-1 overlap;
 //   - the mapping -> pinned copy of a chunk split over a pool of threads (one
 //     thread caps the pipeline well below the PCIe rate);
-//   - H2D and D2H on a copy stream, kernels on a compute stream, ordered by
-//     events; the calling thread never waits on the GPU except for a slot;
+//   - H2D and D2H on two copy streams (so the next chunk's upload never queues
+//     behind this chunk's download, which waits for its kernel), kernels on a
+//     compute stream, ordered by events; the calling thread never waits on
+//     the GPU except for a slot;
 //   - rows handed to the kernel in their stored type (no f32 upcast pass);
 //   - one writer thread that waits on each chunk's D2H event and writes the
 //     chunk at its own offset, so the output never depends on the chunking.
@@ -232,7 +234,7 @@ int elem_size(int src_type) {
 
 struct qs_pipeline {
     int device = 0;
-    hipStream_t copy = nullptr, compute = nullptr;
+    hipStream_t h2d = nullptr, d2h = nullptr, compute = nullptr;
     std::vector<Slot> slots;
     size_t next = 0;
     std::unique_ptr<CopyPool> pool;
@@ -271,7 +273,8 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline*
     if (e != hipSuccess) return fail(QS_EIO, "hipSetDevice(%d): %s", device, hipGetErrorString(e));
     auto p = std::make_unique<qs_pipeline>();
     p->device = device;
-    if ((e = hipStreamCreateWithFlags(&p->copy, hipStreamNonBlocking)) != hipSuccess ||
+    if ((e = hipStreamCreateWithFlags(&p->h2d, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&p->d2h, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipStreamCreateWithFlags(&p->compute, hipStreamNonBlocking)) != hipSuccess) {
         qs_pipeline_destroy(p.release());
         return fail(QS_EIO, "stream creation failed: %s", hipGetErrorString(e));
@@ -348,12 +351,12 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
         p->pool->run(tasks);
         if (nqw) std::memcpy(s.qw_pin.p, imatrix, nqw);
 
-        if (s.used && (e = hipStreamWaitEvent(p->copy, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(s.x_dev.p, s.in_pin.p, nin, hipMemcpyHostToDevice, p->copy)) != hipSuccess)
+        if (s.used && (e = hipStreamWaitEvent(p->h2d, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(s.x_dev.p, s.in_pin.p, nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
             return p->hip_fail(e, "H2D");
-        if (nqw && (e = hipMemcpyAsync(s.qw_dev.p, s.qw_pin.p, nqw, hipMemcpyHostToDevice, p->copy)) != hipSuccess)
+        if (nqw && (e = hipMemcpyAsync(s.qw_dev.p, s.qw_pin.p, nqw, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
             return p->hip_fail(e, "H2D");
-        if ((e = hipEventRecord(s.h2d, p->copy)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipEventRecord(s.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
         if ((e = hipStreamWaitEvent(p->compute, s.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
         if (s.used && (e = hipStreamWaitEvent(p->compute, s.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
         const int rc = qs_quantize(ggml_type, src_type, s.x_dev.p, n, k, in_row,
@@ -364,10 +367,10 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
             return rc;
         }
         if ((e = hipEventRecord(s.kern, p->compute)) != hipSuccess) return p->hip_fail(e, "event");
-        if ((e = hipStreamWaitEvent(p->copy, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(s.out_pin.p, s.out_dev.p, nout, hipMemcpyDeviceToHost, p->copy)) != hipSuccess)
+        if ((e = hipStreamWaitEvent(p->d2h, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(s.out_pin.p, s.out_dev.p, nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
             return p->hip_fail(e, "D2H");
-        if ((e = hipEventRecord(s.d2h, p->copy)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipEventRecord(s.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
         s.used = true;
         s.write_seq = p->writer->push({s.d2h, s.out_pin.p, nout, fd, out_offset + r0 * out_row});
     }
@@ -390,7 +393,8 @@ int qs_pipeline_finish(qs_pipeline* p) {
     if (!p) return fail(QS_EINVAL, "null pipeline");
     p->writer->drain();
     hipError_t e = hipSetDevice(p->device);
-    if (e == hipSuccess) e = hipStreamSynchronize(p->copy);
+    if (e == hipSuccess) e = hipStreamSynchronize(p->h2d);
+    if (e == hipSuccess) e = hipStreamSynchronize(p->d2h);
     if (e == hipSuccess) e = hipStreamSynchronize(p->compute);
     if (e != hipSuccess) return p->hip_fail(e, "device work failed");
     return p->check_writer();
@@ -400,7 +404,8 @@ void qs_pipeline_destroy(qs_pipeline* p) {
     if (!p) return;
     if (p->writer) p->writer->drain();
     (void)hipSetDevice(p->device);
-    if (p->copy) (void)hipStreamSynchronize(p->copy);
+    if (p->h2d) (void)hipStreamSynchronize(p->h2d);
+    if (p->d2h) (void)hipStreamSynchronize(p->d2h);
     if (p->compute) (void)hipStreamSynchronize(p->compute);
     p->writer.reset();
     p->pool.reset();
@@ -415,7 +420,8 @@ void qs_pipeline_destroy(qs_pipeline* p) {
         if (s.kern) (void)hipEventDestroy(s.kern);
         if (s.d2h) (void)hipEventDestroy(s.d2h);
     }
-    if (p->copy) (void)hipStreamDestroy(p->copy);
+    if (p->h2d) (void)hipStreamDestroy(p->h2d);
+    if (p->d2h) (void)hipStreamDestroy(p->d2h);
     if (p->compute) (void)hipStreamDestroy(p->compute);
     delete p;
 }
