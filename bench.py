@@ -68,6 +68,19 @@ def profiled(key: str) -> int | None:
     return None
 
 
+def profiled_valu_per_type() -> dict:
+    """SQ_INSTS_VALU per launch of every per-type kernel (rocprofv3 counter run
+    summarised in profiles/), keyed like per_type."""
+    f = ROOT / "profiles" / "valu_insts_per_type_ffn_9728x2560_2560x9728.md"
+    out = {}
+    if f.exists():
+        for ln in f.read_text().splitlines():
+            if ln.startswith("valu_insts[") and "]:" in ln:
+                key, val = ln[len("valu_insts["):].split("]:")
+                out[key] = float(val)
+    return out
+
+
 def valu_peak(torch, dev, launches: int = 5) -> float:
     """Measured VALU issue rate (wave instructions per second) of a kernel that
     issues only independent f32 multiplies and adds (libqs_calib.so)."""
@@ -353,6 +366,8 @@ def main() -> int:
     achieved = alg / (kms[0] * 1e-3) / 1e9
 
     per_type = {}
+    valu_counts = profiled_valu_per_type()
+    peak_valu = valu_peak(torch, dev)
     sel = [] if args.types == "none" else (list(TYPE_IDS) if args.types == "all"
                                            else args.types.split(","))
     for qtype in sel:
@@ -361,18 +376,23 @@ def main() -> int:
             st, km = time_type(torch, qs, qtype, imat, xs_rot, qws, outs_for(qtype),
                                max(3, args.steps // 4), 1)
             a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
-            per_type[f"{qtype}{'+imat' if imat else ''}"] = {
+            key = f"{qtype}{'+imat' if imat else ''}"
+            insts = valu_counts.get(key)
+            per_type[key] = {
                 "input_GBps": round(2 * n_elems / (st * 1e-3) / 1e9, 2),
                 "ms_per_step": round(st, 4),
                 "kernel_ms": [round(v, 4) for v in km],
                 "hbm_frac": round(a / HBM_PEAK_GBS, 4),
+                # VALU issue rate (SQ_INSTS_VALU per launch over the live launch
+                # time) against the calibration kernel's rate
+                "valu_frac": None if insts is None else
+                round(insts / (sum(km) / len(km) * 1e-3) / peak_valu, 3),
                 "identical_pct_vs_oracle": round(identical_pct(torch, qs, oracle, qtype, imat,
                                                                host, qws), 3),
             }
 
     if "q4_0" in sel:
-        per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, max(3, args.steps // 4))
-    peak_valu = valu_peak(torch, dev)
+        per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
     insts = profiled("valu_insts_per_launch")
 
     line = {

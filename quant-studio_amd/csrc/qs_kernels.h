@@ -139,15 +139,25 @@ __global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
 // ------------------------------------------------------------------
 // shared LDS layout of the superblock kernels
 // ------------------------------------------------------------------
+// The x^2 staging of the weight phase (v, tmp) and the levels and packed
+// blocks of the final phase (L, out) are never live together (every kernel
+// passes several wave_syncs between them), so they share storage: less LDS
+// per workgroup, more resident waves.
 template <int SPW, int BYTES>
 struct alignas(16) SbLds {
-    float v[SPW][QK_K];      // per-value staging for superblock sums
-    float tmp[SPW][40];
+    union {
+        struct {
+            float v[SPW][QK_K];      // per-value staging for superblock sums
+            float tmp[SPW][40];
+        };
+        struct {
+            uint8_t L[SPW][QK_K];
+            uint8_t out[SPW * BYTES + 16];
+        };
+    };
     float sc[SPW][16], mn[SPW][16], sw[SPW][16];
     float hdr[SPW][4];
     int ls[SPW][16], lm[SPW][16];
-    uint8_t L[SPW][QK_K];
-    uint8_t out[SPW * BYTES + 16];
 };
 
 // finish: every valid superblock of the wave has its bytes in s.out
