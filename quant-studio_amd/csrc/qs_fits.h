@@ -60,15 +60,27 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
     for (int s = 0; s < steps.n; s++) {
         den = degen ? 1.0f : mx - mn;
         const float isc = steps.v[s] / den;
-        float La[N], a[N], b[N], c[N];
+        // the three tree sums are formed 8 values at a time (the tree over N
+        // is the trees over its 8-value blocks, then the tree over the block
+        // sums), so only one block of products is live at once
+        constexpr int NB = N / 8;
+        float La[N], sa[NB], sb[NB], sc[NB];
 #pragma unroll
-        for (int i = 0; i < N; i++) {
-            La[i] = clampf(rintf(isc * (x[i] - mn)), 0.0f, fmax);
-            a[i] = w[i] * La[i];
-            b[i] = a[i] * La[i];
-            c[i] = a[i] * x[i];
+        for (int k = 0; k < NB; k++) {
+            float a[8], b[8], c[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = 8 * k + j;
+                La[i] = clampf(rintf(isc * (x[i] - mn)), 0.0f, fmax);
+                a[j] = w[i] * La[i];
+                b[j] = a[j] * La[i];
+                c[j] = a[j] * x[i];
+            }
+            sa[k] = tree_sum(a);
+            sb[k] = tree_sum(b);
+            sc[k] = tree_sum(c);
         }
-        const float sum_l = tree_sum(a), sum_l2 = tree_sum(b), sum_xl = tree_sum(c);
+        const float sum_l = tree_sum(sa), sum_l2 = tree_sum(sb), sum_xl = tree_sum(sc);
         const float D = sum_w * sum_l2 - sum_l * sum_l;
         const float Dsafe = D > 0 ? D : 1.0f;
         float this_scale = (sum_w * sum_xl - sum_x * sum_l) / Dsafe;
@@ -77,14 +89,21 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
             this_scale = sum_xl / fmaxf(sum_l2, F32_TINY);
             this_min = 0.0f;
         }
+        float se[NB];
 #pragma unroll
-        for (int i = 0; i < N; i++) {
-            float d = this_scale * La[i];
-            d = d + this_min;
-            d = d - x[i];
-            t[i] = w[i] * (MAD ? fabsf(d) : d * d);
+        for (int k = 0; k < NB; k++) {
+            float e8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int i = 8 * k + j;
+                float d = this_scale * La[i];
+                d = d + this_min;
+                d = d - x[i];
+                e8[j] = w[i] * (MAD ? fabsf(d) : d * d);
+            }
+            se[k] = tree_sum(e8);
         }
-        const float cur = tree_sum(t);
+        const float cur = tree_sum(se);
         if (D > 0 && cur < best && !degen) {
             best_isc = isc;
             best_mn = mn;
