@@ -188,26 +188,33 @@ QS_DEV float seq_sum(const float (&v)[N]) {
 // torch CPU `.sum(-1)` of a contiguous row of N <= 32 elements: the 8-lane
 // vector cascade. N=32: lane l sums ((v[l]+v[8+l])+v[16+l])+v[24+l];
 // N=16: (v[l]+v[8+l]); N=8: v[l]; then a scalar pass over the 8 lanes from +0.
-template <int N>
-QS_DEV float cascade8_sum(const float (&v)[N]) {
-    static_assert(N == 8 || N == 16 || N == 32, "cascade8_sum: N in {8,16,32}");
+// cascade8_of takes the values as f(0) .. f(N-1), each computed where the sum
+// needs it, so no array of N values is ever live.
+template <int N, typename F>
+QS_DEV float cascade8_of(F&& f) {
+    static_assert(N == 8 || N == 16 || N == 32, "cascade8_of: N in {8,16,32}");
     float fin = 0.0f;
 #pragma unroll
     for (int l = 0; l < 8; l++) {
         float p;
         if constexpr (N == 32) {
-            p = v[l] + v[8 + l];
-            p = p + v[16 + l];
-            p = p + v[24 + l];
+            p = f(l) + f(8 + l);
+            p = p + f(16 + l);
+            p = p + f(24 + l);
         } else if constexpr (N == 16) {
-            p = 0.0f + v[l];
-            p = p + v[8 + l];
+            p = 0.0f + f(l);
+            p = p + f(8 + l);
         } else {
-            p = 0.0f + v[l];
+            p = 0.0f + f(l);
         }
         fin = fin + p;
     }
     return fin;
+}
+
+template <int N>
+QS_DEV float cascade8_sum(const float (&v)[N]) {
+    return cascade8_of<N>([&](int i) { return v[i]; });
 }
 
 // first index of the largest |v| (qx_common.py:26-34); returns the signed value

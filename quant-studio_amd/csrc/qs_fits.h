@@ -136,48 +136,44 @@ QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const fl
     for (int i = 1; i < N; i++) mx = fmaxf(mx, x[i]);
     const bool dead = mx < GROUP_MAX_EPS;
     const float mxs = dead ? 1.0f : mx;
-    float t[N];
 
     float iscale = rdiv(fmax, mxs);
+    float best_mse;
     {
         const float r = 1.0f / iscale;
-#pragma unroll
-        for (int i = 0; i < N; i++) {
+        best_mse = cascade8_of<N>([&](int i) {
             float l0 = rintf(iscale * x[i]);
             float d = x[i] - r * l0;
-            t[i] = w[i] * (d * d);
-        }
+            return w[i] * (d * d);
+        });
     }
-    float best_mse = cascade8_sum(t);
 #pragma unroll 1
     for (int s = 0; s < 8; s++) {
         const float isc = rdiv(steps[s], mxs);
         const float r = 1.0f / isc;
-#pragma unroll
-        for (int i = 0; i < N; i++) {
+        const float mse = cascade8_of<N>([&](int i) {
             float l = fminf(rintf(isc * x[i]), fmax);
             float d = x[i] - r * l;
-            t[i] = w[i] * (d * d);
-        }
-        const float mse = cascade8_sum(t);
+            return w[i] * (d * d);
+        });
         if (mse < best_mse) {
             best_mse = mse;
             iscale = isc;
         }
     }
-    float u[N];
 #pragma unroll
-    for (int i = 0; i < N; i++) {
-        L[i] = fminf(rintf(iscale * x[i]), fmax);
-        t[i] = (w[i] * x[i]) * L[i];
-        u[i] = (w[i] * L[i]) * L[i];
-    }
-    float sumlx = cascade8_sum(t), suml2 = cascade8_sum(u);
+    for (int i = 0; i < N; i++) L[i] = fminf(rintf(iscale * x[i]), fmax);
+    float sumlx = cascade8_of<N>([&](int i) { return (w[i] * x[i]) * L[i]; });
+    float suml2 = cascade8_of<N>([&](int i) { return (w[i] * L[i]) * L[i]; });
 #pragma unroll 1
     for (int pass = 0; pass < 5; pass++) {
 #pragma unroll
         for (int i = 0; i < N; i++) {
-            const float xi = x[i], wi = w[i], Li = L[i];
+            const float xi = x[i], Li = L[i];
+            float wi = w[i];
+            // keeps wi * xi inside the pass: hoisting the N products out of
+            // the loop would hold N more registers for the whole fit
+            asm volatile("" : "+v"(wi));
             const float slx = sumlx - (wi * xi) * Li;
             const float sl2 = suml2 - (wi * Li) * Li;
             const bool ok = slx > 0 && sl2 > 0;

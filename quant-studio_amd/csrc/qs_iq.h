@@ -264,23 +264,8 @@ QS_DEV int sign_bits8(const float (&x)[N], float (&xval)[N]) {
     return s;
 }
 
-// sums of (w*xval)*q and (w*q)*q over the lane's group for grid winners gi[]
-template <int BITS, int NV, int NSUB, int N>
-QS_DEV void iq_sums(const uint32_t* glds, const int (&gi)[NSUB], const float (&w)[N], const float (&xval)[N],
-                    float (&a)[N], float (&b)[N]) {
-#pragma unroll
-    for (int s = 0; s < NSUB; s++) {
-        const Levels<NV> gl = grid_levels<NV>(glds, gi[s]);
-#pragma unroll
-        for (int j = 0; j < NV; j++) {
-            const float q = level<NV>(gl, j);
-            a[NV * s + j] = (w[NV * s + j] * xval[NV * s + j]) * q;
-            b[NV * s + j] = (w[NV * s + j] * q) * q;
-        }
-    }
-}
-
-// the same two sums reduced as tree_sum over the whole group: NV is a power
+// sums of (w*xval)*q and (w*q)*q over the lane's group for grid winners gi[],
+// reduced as tree_sum over the whole group: NV is a power
 // of two, so the group's pairwise tree is each subgroup's own tree followed by
 // a tree over the NSUB subgroup sums; reducing per subgroup keeps 2*NSUB
 // partials live instead of 2*N products
@@ -309,6 +294,36 @@ QS_DEV void iq_tree_sums(const uint32_t* glds, const int (&gi)[NSUB], const floa
         sumqx = tree_sum(sa);
         sumq2 = tree_sum(sb);
     }
+}
+
+// The same two sums reduced as cascade8_sum<32> (torch's `.sum(-1)` over 32):
+// lane l of the 8-wide accumulator is ((v[l] + v[8+l]) + v[16+l]) + v[24+l],
+// i.e. the four 8-value subgroups added in order, then +0 + p[0] + ... + p[7];
+// accumulating subgroup by subgroup keeps 16 partials live instead of 64
+// products.
+QS_DEV void iq_cascade_sums_32(const uint32_t* glds, const int (&gi)[4], const float (&w)[32],
+                               const float (&xval)[32], float& sumqx, float& sumq2) {
+    float pa[8], pb[8];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const Levels<8> gl = grid_levels<8>(glds, gi[s]);
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const float q = level<8>(gl, l);
+            const float a = (w[8 * s + l] * xval[8 * s + l]) * q;
+            const float b = (w[8 * s + l] * q) * q;
+            pa[l] = s == 0 ? a : pa[l] + a;
+            pb[l] = s == 0 ? b : pb[l] + b;
+        }
+    }
+    float fa = 0.0f, fb = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) {
+        fa = fa + pa[l];
+        fb = fb + pb[l];
+    }
+    sumqx = fa;
+    sumq2 = fb;
 }
 
 // superblock scale nibbles: d = max/31, l = clamp(round(0.5*(sc/d - 1)), 0, 15)
@@ -382,7 +397,6 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
     float scale = scale0, best = 0.0f;
     const int zero_gi = T.code0;
     int L[4] = {zero_gi, zero_gi, zero_gi, zero_gi};
-    float ta[32], tb[32];
 #pragma unroll 1
     for (int st = 0; st < sweep.n; st++) {
         const float inv = rdiv(sweep.v[st], eff_safe);
@@ -394,8 +408,8 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
-        iq_sums<2, 8, 4>(glds, gi, w, xval, ta, tb);
-        const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
+        float sumqx, sumq2;
+        iq_cascade_sums_32(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             const float ns = sumqx / fmaxf(sumq2, F32_TINY);
             scale = ns;
@@ -414,8 +428,8 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
         static_for<0, 4>([&](auto S) {
             gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
-        iq_sums<2, 8, 4>(glds, gp, w, xval, ta, tb);
-        const float sumqx = cascade8_sum(ta), sumq2 = cascade8_sum(tb);
+        float sumqx, sumq2;
+        iq_cascade_sums_32(glds, gp, w, xval, sumqx, sumq2);
         if (proj && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
         if (proj) {
 #pragma unroll
