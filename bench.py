@@ -30,13 +30,17 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-# output bytes per 256 input values (per 32 for Q4_0 -> scaled to 256)
+# output bytes per 256 input values (32-value formats: 8 blocks)
 OUT_BYTES_PER_256 = {"q4_0": 144, "q2_k": 84, "q3_k": 110, "q4_k": 144, "q5_k": 176,
                      "q6_k": 210, "iq4_xs": 136, "iq2_xxs": 66, "iq2_xs": 74, "iq2_s": 82,
-                     "iq3_xxs": 98, "iq3_s": 110}
+                     "iq3_xxs": 98, "iq3_s": 110, "q4_1": 160, "q5_0": 176, "q5_1": 192,
+                     "q8_0": 272, "iq4_nl": 144}
 TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14, "iq4_xs": 23,
-            "iq2_xxs": 16, "iq2_xs": 17, "iq2_s": 22, "iq3_xxs": 18, "iq3_s": 21}
+            "iq2_xxs": 16, "iq2_xs": 17, "iq2_s": 22, "iq3_xxs": 18, "iq3_s": 21,
+            "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
 NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
+IGNORE_IMATRIX = {"q4_0", "q4_1", "q5_0", "q5_1", "q8_0"}
+BLOCK_BYTES = {t: (b // 8 if t in IGNORE_IMATRIX | {"iq4_nl"} else b) for t, b in OUT_BYTES_PER_256.items()}
 SHAPES = [(9728, 2560), (2560, 9728)]   # (rows, k)
 ROTATE_BYTES = 1 << 30
 
@@ -154,7 +158,7 @@ def identical_pct(torch, qs, oracle, qtype, imat, host, qws, rows=256):
         got = got.cpu().numpy()
         ref = oracle.quantize(qtype, xb.float().numpy(), qw,
                               n_threads=len(os.sched_getaffinity(0)))
-        bb = OUT_BYTES_PER_256[qtype] if qtype != "q4_0" else 18
+        bb = BLOCK_BYTES[qtype]
         a, b = got.reshape(-1, bb), ref.reshape(-1, bb)
         same += int((a == b).all(1).sum())
         total += a.shape[0]
@@ -371,7 +375,7 @@ def main() -> int:
     sel = [] if args.types == "none" else (list(TYPE_IDS) if args.types == "all"
                                            else args.types.split(","))
     for qtype in sel:
-        modes = (False,) if qtype == "q4_0" else (True,) if qtype in NEEDS_IMATRIX else (False, True)
+        modes = (False,) if qtype in IGNORE_IMATRIX else (True,) if qtype in NEEDS_IMATRIX else (False, True)
         for imat in modes:
             st, km = time_type(torch, qs, qtype, imat, xs_rot, qws, outs_for(qtype),
                                max(3, args.steps // 4), 1)

@@ -45,6 +45,15 @@ extern "C" {
 #define QS_TYPE_IQ3_S 21
 #define QS_TYPE_IQ2_S 22
 #define QS_TYPE_IQ4_XS 23
+/* ggml formats the reference has no quantizer for (its command line stops on
+ * them, quant-studio.py:396-399); the targets of its shape fallback
+ * (kernels/scheme.py:364-384) and of Q4_0/Q5_0 mixes with an imatrix
+ * (scheme.py:521-523) */
+#define QS_TYPE_Q4_1 3
+#define QS_TYPE_Q5_0 6
+#define QS_TYPE_Q5_1 7
+#define QS_TYPE_Q8_0 8
+#define QS_TYPE_IQ4_NL 20
 
 /* source element types accepted as src_type (ggml ids; TORCH_DTYPES
  * kernels/common.py:20-24) */

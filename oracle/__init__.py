@@ -24,7 +24,10 @@ LIB_PATH = HERE / "_build" / "libqs_oracle.so"
 
 TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14,
             "iq2_xxs": 16, "iq2_xs": 17, "iq3_xxs": 18, "iq3_s": 21, "iq2_s": 22,
-            "iq4_xs": 23}
+            "iq4_xs": 23,
+            # ggml formats without a reference module (parity unpinned against
+            # the reference; pinned by known answers and dequantisation bounds)
+            "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
 
 _lib = None
 

@@ -797,6 +797,91 @@ static void iq4_xs_block(const float *x, const float *qw, uint8_t *out) {
 }
 
 /* ------------------------------------------------------------------ */
+/* Q4_1, Q5_0, Q5_1, Q8_0, IQ4_NL: ggml formats the reference has no     */
+/* module for (quant-studio.py:396-399 stops on them). PARITY UNPINNED   */
+/* against the reference, which cannot produce these types. Written from  */
+/* ggml's block layouts and reference quantizers (quantize_row_q4_1_ref,   */
+/* _q5_0_ref, _q5_1_ref, _q8_0_ref; quantize_row_iq4_nl_impl with one     */
+/* block per superblock) in the conventions of the reference's Q4_0       */
+/* (q4_0.py:14-33: first-index signed absmax, IEEE division, one rounding */
+/* per operation) and IQ4_XS (iq4_xs.py:52-76, 149-188: the block search, */
+/* the `.sum(-1)` cascade for sigma2). Pinned instead by known answers,   */
+/* dequantisation bounds and special blocks (tests/test_oracle.py), and   */
+/* IQ4_NL's search by the IQ4_XS golden vectors it shares.               */
+/* ------------------------------------------------------------------ */
+static void q8_0_block(const float *b, uint8_t *out) {
+    float am = 0.0f;
+    for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(b[i]));
+    float d = am / 127.0f;
+    float id = d != 0 ? 1.0f / d : 0.0f;
+    put_f16(out, d);
+    for (int i = 0; i < 32; i++) out[2 + i] = (uint8_t)(int8_t)(int)roundf(b[i] * id);  /* half away from 0 */
+}
+
+/* Q4_1 (nmax 15) and Q5_1 (nmax 31): d = (max - min) / nmax, m = min */
+static void q_1_block(const float *b, uint8_t *out, int nmax) {
+    float mn = b[0], mx = b[0];
+    for (int i = 1; i < 32; i++) { mn = fminf(mn, b[i]); mx = fmaxf(mx, b[i]); }
+    float d = (mx - mn) / (float)nmax;
+    float id = d != 0 ? 1.0f / d : 0.0f;
+    uint8_t q[32];
+    for (int i = 0; i < 32; i++) {
+        float t = b[i] - mn;
+        t = t * id;
+        t = t + 0.5f;
+        q[i] = (uint8_t)fminf(truncf(t), (float)nmax);
+    }
+    put_f16(out, d);
+    put_f16(out + 2, mn);
+    int qs = 4;
+    if (nmax == 31) {
+        uint32_t qh = 0;
+        for (int i = 0; i < 32; i++) qh |= (uint32_t)(q[i] >> 4) << i;
+        for (int j = 0; j < 4; j++) out[4 + j] = (uint8_t)(qh >> (8 * j));
+        qs = 8;
+    }
+    for (int j = 0; j < 16; j++) out[qs + j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+}
+
+static void q5_0_block(const float *b, uint8_t *out) {
+    int im = 0;
+    float am = fabsf(b[0]);
+    for (int i = 1; i < 32; i++)
+        if (fabsf(b[i]) > am) { am = fabsf(b[i]); im = i; }
+    float d = b[im] / -16.0f;
+    float id = d != 0 ? 1.0f / d : 0.0f;
+    uint8_t q[32];
+    for (int i = 0; i < 32; i++) {
+        float t = b[i] * id;
+        t = t + 16.5f;
+        q[i] = (uint8_t)clampf(floorf(t), 0.0f, 31.0f);
+    }
+    put_f16(out, d);
+    uint32_t qh = 0;
+    for (int i = 0; i < 32; i++) qh |= (uint32_t)(q[i] >> 4) << i;
+    for (int j = 0; j < 4; j++) out[2 + j] = (uint8_t)(qh >> (8 * j));
+    for (int j = 0; j < 16; j++) out[6 + j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+}
+
+static void iq4_nl_block(const float *x, const float *qw, uint8_t *out) {
+    float w[32];
+    if (!qw) {
+        for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
+    } else {
+        float sigma2 = (2.0f * sumsq_c8(x, 32)) / 32.0f;
+        for (int i = 0; i < 32; i++) {
+            float t = x[i] * x[i];
+            w[i] = qw[i] * SQRT(sigma2 + t);
+        }
+    }
+    float d = iq4_search_scale(x, w);
+    float id = d != 0 ? 1.0f / d : 0.0f;
+    put_f16(out, d);
+    for (int j = 0; j < 16; j++)
+        out[2 + j] = (uint8_t)(iq4_best_index(id * x[j]) | (iq4_best_index(id * x[j + 16]) << 4));
+}
+
+/* ------------------------------------------------------------------ */
 /* dispatch                                                            */
 /* ------------------------------------------------------------------ */
 #include "qs_oracle_iq.c"
@@ -815,6 +900,11 @@ static int block_info(int type, int *blk, int *bytes) {
     case QSO_IQ2_S: *blk = 256; *bytes = 82; return 0;
     case QSO_IQ3_XXS: *blk = 256; *bytes = 98; return 0;
     case QSO_IQ3_S: *blk = 256; *bytes = 110; return 0;
+    case QSO_Q4_1: *blk = 32; *bytes = 20; return 0;
+    case QSO_Q5_0: *blk = 32; *bytes = 22; return 0;
+    case QSO_Q5_1: *blk = 32; *bytes = 24; return 0;
+    case QSO_Q8_0: *blk = 32; *bytes = 34; return 0;
+    case QSO_IQ4_NL: *blk = 32; *bytes = 18; return 0;
     default: return -1;
     }
 }
@@ -847,6 +937,11 @@ int qso_quantize(int type, const float *x, int64_t n_rows, int64_t k, const floa
         case QSO_Q5_K: q45_k_block(xb, qb, ob, 31); break;
         case QSO_Q6_K: q6_k_block(xb, qb, ob); break;
         case QSO_IQ4_XS: iq4_xs_block(xb, qb, ob); break;
+        case QSO_Q4_1: q_1_block(xb, ob, 15); break;
+        case QSO_Q5_0: q5_0_block(xb, ob); break;
+        case QSO_Q5_1: q_1_block(xb, ob, 31); break;
+        case QSO_Q8_0: q8_0_block(xb, ob); break;
+        case QSO_IQ4_NL: iq4_nl_block(xb, qb, ob); break;
         default: bad |= qs_oracle_iq(type, xb, qb, ob); break;
         }
     }

@@ -24,7 +24,9 @@ extern "C" {
 enum {
     QSO_Q4_0 = 2, QSO_Q2_K = 10, QSO_Q3_K = 11, QSO_Q4_K = 12, QSO_Q5_K = 13,
     QSO_Q6_K = 14, QSO_IQ2_XXS = 16, QSO_IQ2_XS = 17, QSO_IQ3_XXS = 18,
-    QSO_IQ3_S = 21, QSO_IQ2_S = 22, QSO_IQ4_XS = 23
+    QSO_IQ3_S = 21, QSO_IQ2_S = 22, QSO_IQ4_XS = 23,
+    /* no reference module; parity unpinned against the reference */
+    QSO_Q4_1 = 3, QSO_Q5_0 = 6, QSO_Q5_1 = 7, QSO_Q8_0 = 8, QSO_IQ4_NL = 20
 };
 
 /* bytes of one quantized row of k elements, or -1 for an unsupported type / k */

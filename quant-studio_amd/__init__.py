@@ -52,6 +52,23 @@ class QuantSpecError(RuntimeError):
     """A quantizer call was rejected or failed in the HIP library."""
 
 
+def _bind_torch_hip_runtime() -> None:
+    """torch's ROCm wheel carries its own HIP runtime (torch/lib/libamdhip64.so,
+    soname libamdhip64.so.7), which torch's libraries load by file name. If this
+    library were loaded first it would bind the system copy, and a later
+    `import torch` would map a second HIP and HSA runtime into the process,
+    after which this library's device calls fail. So when torch is installed,
+    its runtime is loaded first (without importing torch) and this library binds
+    to it; in any import order the process then has one HIP runtime."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    for loc in (spec.submodule_search_locations or []) if spec else []:
+        rt = Path(loc) / "lib" / "libamdhip64.so"
+        if rt.exists():
+            ctypes.CDLL(str(rt), mode=ctypes.RTLD_GLOBAL)
+            return
+
+
 def library() -> ctypes.CDLL:
     """Load libqs_hip.so (built in-tree by build.py); raises if it is missing."""
     global _lib
@@ -59,6 +76,7 @@ def library() -> ctypes.CDLL:
         if not LIB_PATH.exists():
             raise ImportError(f"{LIB_PATH} is missing: build it with "
                               "quant-studio_amd/build.py (or __graft_entry__.build())")
+        _bind_torch_hip_runtime()
         L = ctypes.CDLL(str(LIB_PATH))
         L.qs_abi_version.restype = ctypes.c_int
         L.qs_type_supported.restype = ctypes.c_int
@@ -160,7 +178,8 @@ class QuantSpec:
 def _kernel_factory(ggml_type: GGMLQuantizationType, uses_imatrix: bool):
     def make_kernel(device, qw):
         import torch
-        q = qw if uses_imatrix else None    # Q4_0 ignores an imatrix (q4_0.py:36-37)
+        q = qw if uses_imatrix else None    # Q4_0 ignores an imatrix (q4_0.py:36-37), as do
+                                            # the other 32-value integer formats
         if q is not None:
             q = q.to(device=device, dtype=torch.float32).contiguous()
         return lambda x: quantize(ggml_type, x, q)
@@ -186,6 +205,13 @@ _SPECS = [
     ("iq2_s", _T.IQ2_S, _F.MOSTLY_IQ2_S, 64, True, True),
     ("iq3_xxs", _T.IQ3_XXS, _F.MOSTLY_IQ3_XXS, 64, True, True),
     ("iq3_s", _T.IQ3_S, _F.MOSTLY_IQ3_S, 64, False, True),
+    # ggml formats the reference has no module for (quant-studio.py:396-399
+    # stops on them); working-set sizes as for the reference's Q4_0 and IQ4_XS
+    ("q4_1", _T.Q4_1, _F.MOSTLY_Q4_1, 16, False, False),
+    ("q5_0", _T.Q5_0, _F.MOSTLY_Q5_0, 16, False, False),
+    ("q5_1", _T.Q5_1, _F.MOSTLY_Q5_1, 16, False, False),
+    ("q8_0", _T.Q8_0, _F.MOSTLY_Q8_0, 16, False, False),
+    ("iq4_nl", _T.IQ4_NL, _F.MOSTLY_IQ4_NL, 24, False, True),
 ]
 ALL_SPECS: dict[str, QuantSpec] = {
     name: QuantSpec(t, f, bpe, needs, _kernel_factory(t, uses), uses)

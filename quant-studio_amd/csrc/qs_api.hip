@@ -68,6 +68,14 @@ constexpr TypeInfo kTypes[] = {
     {QS_TYPE_IQ2_S, "iq2_s", 256, 82, true, true},
     {QS_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, true, true},
     {QS_TYPE_IQ3_S, "iq3_s", 256, 110, false, true},
+    // ggml formats without a reference module (quant-studio.py:396-399 stops
+    // on them): block layouts from the GGUF format; the imatrix is used by
+    // IQ4_NL only (the 32-value integer formats ignore it, as Q4_0 does)
+    {QS_TYPE_Q4_1, "q4_1", 32, 20, false, false},
+    {QS_TYPE_Q5_0, "q5_0", 32, 22, false, false},
+    {QS_TYPE_Q5_1, "q5_1", 32, 24, false, false},
+    {QS_TYPE_Q8_0, "q8_0", 32, 34, false, false},
+    {QS_TYPE_IQ4_NL, "iq4_nl", 32, 18, false, true},
 };
 
 const TypeInfo* find_type(int id) {
@@ -277,15 +285,27 @@ qs::Steps qx_steps(int nmax) {
     return s;
 }
 
+template <int SRC, qs::B32 T>
+void launch_b32(const qs::KArgs& a, hipStream_t st) {
+    const unsigned g = (unsigned)((a.n_units + qs::Q40_BLOCKS_PER_WG - 1) / qs::Q40_BLOCKS_PER_WG);
+    hipLaunchKernelGGL((qs::k_b32<SRC, T>), dim3(g), dim3(256), 0, st, a);
+}
+
 template <int SRC>
 void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
                  const std::array<qs::IqTabDev, IQT_N>& tabs) {
     using namespace qs;
     const unsigned sb8 = (unsigned)((a.n_units + 7) / 8), sb4 = (unsigned)((a.n_units + 3) / 4);
     switch (type) {
-    case QS_TYPE_Q4_0: {
-        const unsigned g = (unsigned)((a.n_units + Q40_BLOCKS_PER_WG - 1) / Q40_BLOCKS_PER_WG);
-        hipLaunchKernelGGL(k_q4_0<SRC>, dim3(g), dim3(256), 0, st, a);
+    case QS_TYPE_Q4_0: launch_b32<SRC, B32::Q4_0>(a, st); break;
+    case QS_TYPE_Q4_1: launch_b32<SRC, B32::Q4_1>(a, st); break;
+    case QS_TYPE_Q5_0: launch_b32<SRC, B32::Q5_0>(a, st); break;
+    case QS_TYPE_Q5_1: launch_b32<SRC, B32::Q5_1>(a, st); break;
+    case QS_TYPE_Q8_0: launch_b32<SRC, B32::Q8_0>(a, st); break;
+    case QS_TYPE_IQ4_NL: {
+        const unsigned g = (unsigned)((a.n_units + 63) / 64);
+        if (imat) hipLaunchKernelGGL((k_iq4_nl<SRC, true>), dim3(g), dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((k_iq4_nl<SRC, false>), dim3(g), dim3(64), 0, st, a);
         break;
     }
     case QS_TYPE_Q4_K:

@@ -1,8 +1,9 @@
-// Quantizer kernels for Q4_0, Q2_K..Q6_K and IQ4_XS on gfx950.
+// Quantizer kernels for the 32-value block formats (Q4_0, Q4_1, Q5_0, Q5_1,
+// Q8_0), Q2_K..Q6_K, IQ4_XS and IQ4_NL on gfx950.
 //
-// Q4_0 is HBM-bound: four lanes per 32-value block, 16-byte coalesced loads,
-// a cross-lane first-index absmax, output staged through LDS and stored with
-// coalesced dwords.
+// The 32-value formats are HBM-bound: four lanes per block, 16-byte coalesced
+// loads, cross-lane absmax / min / max, output staged through LDS and stored
+// with coalesced words.
 //
 // The K-quants and IQ4_XS are VALU-bound (their scale searches cost hundreds of
 // f32 ops per value): one lane per 16/32-value group keeps the group and its
@@ -31,15 +32,168 @@ struct QpSteps {
 };
 
 // ------------------------------------------------------------------
-// Q4_0  (q4_0.py:14-33)
+// 32-value block formats: Q4_0 (q4_0.py:14-33) and the ggml formats the
+// reference has no module for (its command line stops on them,
+// quant-studio.py:396-399): Q4_1, Q5_0, Q5_1, Q8_0. Those follow ggml's block
+// layouts and reference quantizers (quantize_row_q4_1_ref ... _q8_0_ref) with
+// the conventions of the reference's Q4_0: first-index signed absmax, IEEE
+// division, one rounding per operation. The imatrix is not used by any of
+// them (as for the reference's Q4_0, q4_0.py:36-37).
 // ------------------------------------------------------------------
+enum class B32 { Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 };
+
+template <B32 T>
+constexpr int b32_bytes() {
+    return T == B32::Q4_0 ? 18 : T == B32::Q4_1 ? 20 : T == B32::Q5_0 ? 22 : T == B32::Q5_1 ? 24 : 34;
+}
+
 constexpr int Q40_TILE = 64;                   // blocks per 256-thread tile (4 lanes per block)
 constexpr int Q40_TILES = 4;                   // tiles per workgroup, loaded before any compute
 constexpr int Q40_BLOCKS_PER_WG = Q40_TILE * Q40_TILES;
 
-template <int SRC>
-__global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t stage[Q40_BLOCKS_PER_WG * 18];
+// signed value of the largest |x| of the block, first index wins (argmax of
+// abs): the lane's max |x|, then its first value of that magnitude, then the
+// lowest quarter holding the block's max
+QS_DEV float quad_absmax_first(const float (&x)[8], int q) {
+    float am = fabsf(x[0]);
+#pragma unroll
+    for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
+    float mv = x[7];
+#pragma unroll
+    for (int i = 6; i >= 0; i--) mv = fabsf(x[i]) == am ? x[i] : mv;
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+        const float pam = __shfl_xor(am, m, 4);
+        const float pmv = __shfl_xor(mv, m, 4);
+        const bool take = pam > am || (pam == am && (q ^ m) < q);
+        am = take ? pam : am;
+        mv = take ? pmv : mv;
+    }
+    return mv;
+}
+
+QS_DEV void quad_min_max(const float (&x)[8], float& mn, float& mx) {
+    mn = x[0];
+    mx = x[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) {
+        mn = fminf(mn, x[i]);
+        mx = fmaxf(mx, x[i]);
+    }
+#pragma unroll
+    for (int m = 1; m <= 2; m <<= 1) {
+        mn = fminf(mn, __shfl_xor(mn, m, 4));
+        mx = fmaxf(mx, __shfl_xor(mx, m, 4));
+    }
+}
+
+// qs[j] = L[j] & 15 | (L[j+16] & 15) << 4 from the lanes' 8 nibbles: quarters
+// 0/1 hold the low halves and take the high nibbles of quarters 2/3; writes
+// 8 bytes at o (q < 2), o 2-byte aligned
+QS_DEV void quad_store_nibbles(uint32_t nib, int q, uint8_t* o) {
+    const uint32_t hi = __shfl_xor(nib, 2, 4);
+    if (q < 2) {
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w0 |= (((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4)) << (8 * i);
+            w1 |= (((nib >> (4 * (i + 4))) & 15u) | (((hi >> (4 * (i + 4))) & 15u) << 4)) << (8 * i);
+        }
+        uint16_t* o16 = reinterpret_cast<uint16_t*>(o + 8 * q);
+        o16[0] = (uint16_t)w0;
+        o16[1] = (uint16_t)(w0 >> 16);
+        o16[2] = (uint16_t)w1;
+        o16[3] = (uint16_t)(w1 >> 16);
+    }
+}
+
+// one block, four lanes: lane quarter q holds values 8q..8q+7 and writes its
+// share of the block's bytes at o (LDS, block start, 2-byte aligned)
+template <B32 T>
+QS_DEV void b32_block(const float (&x)[8], int q, uint8_t* o) {
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(o);
+    if constexpr (T == B32::Q4_0 || T == B32::Q5_0) {
+        // d = max / -8 (q4_0.py:24) or max / -16: exact scalings by a power of two
+        const float mv = quad_absmax_first(x, q);
+        const float d = T == B32::Q4_0 ? mv * -0.125f : mv * -0.0625f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        constexpr float OFF = T == B32::Q4_0 ? 8.5f : 16.5f;
+        constexpr float TOP = T == B32::Q4_0 ? 15.5f : 31.5f;
+        uint32_t nib = 0, h5 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float t = x[i] * id;
+            t = t + OFF;
+            // clamp(floor(t), 0, top) == trunc(clamp(t, 0, top + 0.5)): truncation
+            // is floor on [0, top + 0.5] (NaN clamps to 0 either way)
+            const uint32_t qv = (uint32_t)clampf(t, 0.0f, TOP);
+            nib |= (qv & 15u) << (4 * i);
+            h5 |= (qv >> 4) << i;
+        }
+        if (q == 0) o16[0] = (uint16_t)f16_bits(d);
+        if constexpr (T == B32::Q4_0) {
+            quad_store_nibbles(nib, q, o + 2);
+        } else {
+            o[2 + q] = (uint8_t)h5;                 // qh: bit j is bit 4 of L[j]
+            quad_store_nibbles(nib, q, o + 6);
+        }
+    } else if constexpr (T == B32::Q4_1 || T == B32::Q5_1) {
+        // d = (max - min) / nmax, m = min; L = min(nmax, trunc((x - min) * id + 0.5))
+        constexpr float NMAX = T == B32::Q4_1 ? 15.0f : 31.0f;
+        float mn, mx;
+        quad_min_max(x, mn, mx);
+        const float d = (mx - mn) / NMAX;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t nib = 0, h5 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float t = x[i] - mn;
+            t = t * id;
+            t = t + 0.5f;
+            const uint32_t qv = (uint32_t)clampf(t, 0.0f, NMAX);
+            nib |= (qv & 15u) << (4 * i);
+            h5 |= (qv >> 4) << i;
+        }
+        if (q == 0) {
+            o16[0] = (uint16_t)f16_bits(d);
+            o16[1] = (uint16_t)f16_bits(mn);
+        }
+        if constexpr (T == B32::Q4_1) {
+            quad_store_nibbles(nib, q, o + 4);
+        } else {
+            o[4 + q] = (uint8_t)h5;
+            quad_store_nibbles(nib, q, o + 8);
+        }
+    } else {
+        // Q8_0: d = amax / 127, q = round half away from zero (C roundf)
+        float am = fabsf(x[0]);
+#pragma unroll
+        for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
+#pragma unroll
+        for (int m = 1; m <= 2; m <<= 1) am = fmaxf(am, __shfl_xor(am, m, 4));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t w[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int v = (int)roundf(x[i] * id);
+            w[i >> 2] |= ((uint32_t)v & 0xffu) << (8 * (i & 3));
+        }
+        if (q == 0) o16[0] = (uint16_t)f16_bits(d);
+        uint16_t* p = reinterpret_cast<uint16_t*>(o + 2 + 8 * q);
+        p[0] = (uint16_t)w[0];
+        p[1] = (uint16_t)(w[0] >> 16);
+        p[2] = (uint16_t)w[1];
+        p[3] = (uint16_t)(w[1] >> 16);
+    }
+}
+
+// HBM-bound: four lanes per 32-value block, four tiles of 16-byte loads in
+// flight per lane, output staged through LDS and stored with 16-byte words
+template <int SRC, B32 T>
+__global__ __launch_bounds__(256) void k_b32(KArgs a) {
+    constexpr int BYTES = b32_bytes<T>();
+    __shared__ __attribute__((aligned(16))) uint8_t stage[Q40_BLOCKS_PER_WG * BYTES];
     const int tid = threadIdx.x;
     const int q = tid & 3;                       // quarter of the block: values 8q..8q+7
     const int64_t b0 = (int64_t)blockIdx.x * Q40_BLOCKS_PER_WG;
@@ -62,63 +216,11 @@ __global__ __launch_bounds__(256) void k_q4_0(KArgs a) {
         load_elems<SRC, true, 8>(a.src, e, x[u]);
     }
 #pragma unroll
-    for (int u = 0; u < Q40_TILES; u++) {
-        // signed value of the largest |x|, first index wins (argmax of abs):
-        // the lane's max |x|, then its first value of that magnitude, then
-        // the lowest quarter holding the block's max
-        float am = fabsf(x[u][0]);
-#pragma unroll
-        for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[u][i]));
-        float mv = x[u][7];
-#pragma unroll
-        for (int i = 6; i >= 0; i--) mv = fabsf(x[u][i]) == am ? x[u][i] : mv;
-#pragma unroll
-        for (int m = 1; m <= 2; m <<= 1) {
-            const float pam = __shfl_xor(am, m, 4);
-            const float pmv = __shfl_xor(mv, m, 4);
-            const bool take = pam > am || (pam == am && (q ^ m) < q);
-            am = take ? pam : am;
-            mv = take ? pmv : mv;
-        }
-        const float d = mv * -0.125f;             // == mv / -8.0f: exact scaling by a power of two
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint32_t nib = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float t = x[u][i] * id;
-            t = t + 8.5f;
-            // clamp(floor(t), 0, 15) == trunc(clamp(t, 0, 15.5)): truncation is
-            // floor on [0, 15.5] (NaN clamps to 0 either way)
-            const uint32_t qv = (uint32_t)clampf(t, 0.0f, 15.5f);
-            nib |= qv << (4 * i);
-        }
-        // qs[j] = q[j] | q[j+16] << 4: quarters 0/1 take the high nibbles of 2/3
-        const uint32_t hi = __shfl_xor(nib, 2, 4);
-        uint8_t* o = stage + (u * Q40_TILE + (tid >> 2)) * 18;
-        if (q == 0) {
-            const uint32_t h = f16_bits(d);
-            o[0] = (uint8_t)h;
-            o[1] = (uint8_t)(h >> 8);
-        }
-        if (q < 2) {
-            uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                w0 |= (((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4)) << (8 * i);
-                w1 |= (((nib >> (4 * (i + 4))) & 15u) | (((hi >> (4 * (i + 4))) & 15u) << 4)) << (8 * i);
-            }
-            // 2-byte aligned destination: four 16-bit LDS stores
-            uint16_t* o16 = reinterpret_cast<uint16_t*>(o + 2 + 8 * q);
-            o16[0] = (uint16_t)w0;
-            o16[1] = (uint16_t)(w0 >> 16);
-            o16[2] = (uint16_t)w1;
-            o16[3] = (uint16_t)(w1 >> 16);
-        }
-    }
+    for (int u = 0; u < Q40_TILES; u++) b32_block<T>(x[u], q, stage + (u * Q40_TILE + (tid >> 2)) * BYTES);
     __syncthreads();
     const int64_t nvalid = min((int64_t)Q40_BLOCKS_PER_WG, a.n_units - b0);
-    const int nbytes = (int)nvalid * 18;
-    uint8_t* dbase = a.dst + b0 * 18;
+    const int nbytes = (int)nvalid * BYTES;
+    uint8_t* dbase = a.dst + b0 * BYTES;
     if ((reinterpret_cast<uintptr_t>(dbase) & 15) == 0) {
         const int n16 = nbytes >> 4;
         const uint4* s16 = reinterpret_cast<const uint4*>(stage);
@@ -638,6 +740,65 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     }
     wave_sync();
     sb_store(s, a);
+}
+
+// ------------------------------------------------------------------
+// IQ4_NL: no module in the reference (its command line stops on the type,
+// quant-studio.py:396-399). ggml's quantize_row_iq4_nl_impl with one block
+// per superblock, restated with the reference's IQ4_XS conventions: weights
+// x^2 or qw*sqrt(2*sum(x^2)/32 + x^2) (the `.sum(-1)` cascade over the block,
+// as iq4_xs.py:158-160 over 256), the IQ4_XS block search (iq4_xs.py:52-76),
+// d = fp16(scale), levels reprojected at 1/scale with the same LUT rule.
+// One lane per block, 64 blocks per workgroup.
+// ------------------------------------------------------------------
+template <int SRC, bool IMAT>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_nl(KArgs a) {
+    constexpr int BYTES = 18;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[64 * BYTES];
+    __shared__ float2 iq4tab[256];
+    __shared__ uint8_t iq4mu[256];
+    iq4_build_table(iq4tab, iq4mu);
+    const int lane = threadIdx.x;
+    const int64_t b0 = (int64_t)blockIdx.x * 64;
+    int64_t b = b0 + lane;
+    b = b < a.n_units ? b : a.n_units - 1;
+    const int64_t row = b / a.units_per_row;
+    const int64_t col = (b - row * a.units_per_row) * 32;
+    float x[32], w[32];
+    load_elems<SRC, true, 32>(a.src, row * a.stride + col, x);
+    if constexpr (IMAT) {
+        const float sigma2 = (2.0f * cascade8_of<32>([&](int i) { return x[i] * x[i]; })) / 32.0f;
+        imatrix_weights<32>(a.qw + col, sigma2, x, a.sqrt_down, w);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
+    }
+    wave_sync();                                 // iq4tab ready
+    const float scale = iq4_scale_search(x, w, iq4tab);
+    const float id = scale != 0.0f ? 1.0f / scale : 0.0f;
+    uint8_t* o = stage + lane * BYTES;
+    const uint32_t h = f16_bits(scale);
+    o[0] = (uint8_t)h;
+    o[1] = (uint8_t)(h >> 8);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int lo = iq4_project_index(id * x[j], iq4tab, iq4mu);
+        const int hi = iq4_project_index(id * x[j + 16], iq4tab, iq4mu);
+        o[2 + j] = (uint8_t)(lo | (hi << 4));
+    }
+    wave_sync();
+    const int64_t nvalid = min((int64_t)64, a.n_units - b0);
+    const int nbytes = (int)nvalid * BYTES;
+    uint8_t* dbase = a.dst + b0 * BYTES;
+    if ((reinterpret_cast<uintptr_t>(dbase) & 3) == 0) {
+        const int nw = nbytes >> 2;
+        const uint32_t* s4 = reinterpret_cast<const uint32_t*>(stage);
+        uint32_t* d4 = reinterpret_cast<uint32_t*>(dbase);
+        for (int t = lane; t < nw; t += 64) d4[t] = s4[t];
+        for (int t = (nw << 2) + lane; t < nbytes; t += 64) dbase[t] = stage[t];
+    } else {
+        for (int t = lane; t < nbytes; t += 64) dbase[t] = stage[t];
+    }
 }
 
 }  // namespace qs

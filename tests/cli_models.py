@@ -80,3 +80,14 @@ def imatrix_for(path: Path, names_k: dict[str, int], seed: int = 7, n_mat: dict 
         values[name] = (s.reshape(m, k) / cnt[:, None]).reshape(-1)
     io.write_gguf(path, "imatrix", [KV("general.type", VT.STRING, "imatrix")], tensors)
     return values
+
+
+def fallback_model(path: Path) -> dict[str, np.ndarray]:
+    """Tensors whose rows (288 values) are a multiple of 32 but not of 256."""
+    rng = np.random.default_rng(3)
+    names = ["blk.0.attn_q.weight", "blk.0.attn_k.weight", "blk.0.attn_v.weight",
+             "blk.0.ffn_down.weight", "blk.0.ffn_up.weight"]
+    arrays = {n: (rng.standard_normal((48, 288)) * 0.02).astype(np.float32) for n in names}
+    io.write_gguf(path, "llama", [KV("llama.block_count", VT.UINT32, 1)],
+                  [(n, (288, 48), GT.F32, a) for n, a in arrays.items()])
+    return arrays

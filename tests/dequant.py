@@ -1,9 +1,10 @@
-"""Dequantizers for the 12 block formats (numpy, test infrastructure).
+"""Dequantizers for the 17 block formats (numpy, test infrastructure).
 
 Written from the public ggml block layouts (the packing each reference module
 writes: q4_0.py:30-32, q2_k.py:74-80, q3_k.py:61-77, q4_k.py:70-78,
 q5_k.py:70-81, q6_k.py:55-64, iq4_xs.py:178-187, iq2.py:87-108,
-iq2_xs.py:50-69, iq2_s.py:44-62, iq3_xxs.py:104-134, iq3_s.py:100-140) and
+iq2_xs.py:50-69, iq2_s.py:44-62, iq3_xxs.py:104-134, iq3_s.py:100-140; for
+Q4_1, Q5_0, Q5_1, Q8_0 and IQ4_NL the GGUF block layouts) and
 ggml's reconstruction of each format, which the reference does not contain
 (its dev harness calls gguf-py's `dequantize`, tools/dev_harness.py:23, :108;
 gguf-py is not available here). Used for the weighted-MSE tie rule and the
@@ -73,6 +74,46 @@ def deq_q4_0(data):
     qs = b[:, 2:18].astype(np.int64)
     q = np.concatenate([qs & 15, qs >> 4], 1)
     return d[:, None] * (q - 8)
+
+
+def _nibbles32(qs: np.ndarray) -> np.ndarray:
+    """(n, 32) 4-bit values of a 16-byte `q[j] | q[j+16] << 4` field."""
+    qs = qs.astype(np.int64)
+    return np.concatenate([qs & 15, qs >> 4], 1)
+
+
+def _qh32(qh4: np.ndarray) -> np.ndarray:
+    """(n, 32) fifth bits: bit j of the little-endian 32-bit qh field."""
+    qh = qh4.copy().view(np.uint32).astype(np.int64)[:, 0]
+    return (qh[:, None] >> np.arange(32)) & 1
+
+
+# ggml formats the reference has no quantizer for (ggml's dequantize_row_*)
+def deq_q4_1(data):
+    b = _blocks(data, 20)
+    return _f16(b, 0)[:, None] * _nibbles32(b[:, 4:20]) + _f16(b, 2)[:, None]
+
+
+def deq_q5_0(data):
+    b = _blocks(data, 22)
+    q = _nibbles32(b[:, 6:22]) | (_qh32(b[:, 2:6]) << 4)
+    return _f16(b, 0)[:, None] * (q - 16)
+
+
+def deq_q5_1(data):
+    b = _blocks(data, 24)
+    q = _nibbles32(b[:, 8:24]) | (_qh32(b[:, 4:8]) << 4)
+    return _f16(b, 0)[:, None] * q + _f16(b, 2)[:, None]
+
+
+def deq_q8_0(data):
+    b = _blocks(data, 34)
+    return _f16(b, 0)[:, None] * b[:, 2:34].view(np.int8).astype(np.float64)
+
+
+def deq_iq4_nl(data):
+    b = _blocks(data, 18)
+    return _f16(b, 0)[:, None] * IQ4NL[_nibbles32(b[:, 2:18])]
 
 
 def deq_q2_k(data):
@@ -267,7 +308,11 @@ def deq_iq3_s(data):
 
 DEQUANT = {"q4_0": deq_q4_0, "q2_k": deq_q2_k, "q3_k": deq_q3_k, "q4_k": deq_q4_k,
            "q5_k": deq_q5_k, "q6_k": deq_q6_k, "iq4_xs": deq_iq4_xs, "iq2_xxs": deq_iq2_xxs,
-           "iq2_xs": deq_iq2_xs, "iq2_s": deq_iq2_s, "iq3_xxs": deq_iq3_xxs, "iq3_s": deq_iq3_s}
+           "iq2_xs": deq_iq2_xs, "iq2_s": deq_iq2_s, "iq3_xxs": deq_iq3_xxs, "iq3_s": deq_iq3_s,
+           "q4_1": deq_q4_1, "q5_0": deq_q5_0, "q5_1": deq_q5_1, "q8_0": deq_q8_0,
+           "iq4_nl": deq_iq4_nl}
+
+BLOCK = {t: (32 if t in ("q4_0", "q4_1", "q5_0", "q5_1", "q8_0", "iq4_nl") else 256) for t in DEQUANT}
 
 
 def dequantize(qtype: str, data: np.ndarray, n_rows: int) -> np.ndarray:
@@ -280,5 +325,5 @@ def block_weighted_mse(qtype: str, data: np.ndarray, x: np.ndarray, qw: np.ndarr
     xhat = dequantize(qtype, data, n)
     w = np.ones(k) if qw is None else qw[:k].astype(np.float64)
     e = w[None, :] * (x.astype(np.float64) - xhat) ** 2
-    blk = 32 if qtype == "q4_0" else 256
+    blk = BLOCK[qtype]
     return e.reshape(n, k // blk, blk).sum(-1).reshape(-1)

@@ -6,6 +6,8 @@ from __future__ import annotations
 
 import ctypes
 import re
+import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -112,3 +114,16 @@ def test_pipeline_rejects_bad_arguments_without_device_work(qs):
     assert L.qs_pipeline_finish(None) == -22
     L.qs_pipeline_destroy(None)
     assert L.qs_device_count() >= 0
+
+
+def test_one_hip_runtime_in_any_import_order():
+    """Package first, torch second: the process must map a single HIP runtime
+    (two runtimes make the library's device calls fail)."""
+    code = ("import importlib, sys; sys.path.insert(0, sys.argv[1]); "
+            "importlib.import_module('quant-studio_amd'); import torch; "
+            "m = open('/proc/self/maps').read().splitlines(); "
+            "print(len({l.split()[-1] for l in m if 'libamdhip64' in l}))")
+    r = subprocess.run([sys.executable, "-c", code, str(ROOT)], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.strip() == "1"

@@ -12,7 +12,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from cli_models import GT, KV, VT, imatrix_for, io, small_model
+from cli_models import GT, KV, VT, fallback_model, imatrix_for, io, small_model
 
 ROOT = Path(__file__).resolve().parent.parent
 CLI = [sys.executable, str(ROOT / "quant-studio.py")]
@@ -81,7 +81,7 @@ def test_dry_run_plan(tmp_path):
     (["q4_0", "--allow-requantize"], "--allow-requantize is not supported"),
     (["q4_0", "--keep-split"], "--keep-split is not supported"),
     (["NOPE"], "unknown quantization scheme"),
-    (["Q8_0"], "not supported by quant-studio"),
+    (["IQ1_S"], "not supported by quant-studio"),
     (["q4_0", "8"], "nthreads argument is not supported"),
     (["iq2_xxs"], "require importance matrix data"),
     (["q4_0", "--tensor-type", "attn"], "expected name=ggml_type"),
@@ -113,13 +113,44 @@ def test_fallback_to_a_type_without_kernel_is_an_error(tmp_path):
     assert r.returncode != 0 and "F16 for 1 tensors" in r.stderr
 
 
-def test_missing_kernel_type_is_an_error(tmp_path):
-    # Q4_0 with an imatrix asks for Q4_1 on the first ffn_down layers (no kernel)
-    src = tmp_path / "in.gguf"
-    io.write_gguf(src, "llama", [KV("llama.block_count", VT.UINT32, 8)],
+def ffn_down_model(path: Path, n_layer: int = 8) -> None:
+    io.write_gguf(path, "llama", [KV("llama.block_count", VT.UINT32, n_layer)],
                   [(f"blk.{i}.ffn_down.weight", (256, 32), GT.F32,
-                    np.zeros((32, 256), np.float32)) for i in range(8)])
+                    np.zeros((32, 256), np.float32)) for i in range(n_layer)])
+
+
+def test_missing_kernel_type_is_an_error(tmp_path):
+    # an override to a type without a quantizer (IQ1_S)
+    src = tmp_path / "in.gguf"
+    ffn_down_model(src)
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--tensor-type", "ffn_down=iq1_s", "--dry-run",
+                check=False)
+    assert r.returncode != 0 and "needs kernel types" in r.stderr and "IQ1_S" in r.stderr
+
+
+def test_q4_0_with_imatrix_uses_q4_1_on_the_first_ffn_down_layers(tmp_path):
+    # scheme.py:521-523: i_layer < n_layer / 8 with an imatrix -> Q4_1
+    src = tmp_path / "in.gguf"
+    ffn_down_model(src)
     im = tmp_path / "im.gguf"
     imatrix_for(im, {f"blk.{i}.ffn_down.weight": 256 for i in range(8)})
-    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--imatrix", im, "--dry-run", check=False)
-    assert r.returncode != 0 and "Q4_1" in r.stderr
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--imatrix", im, "--dry-run")
+    lines = {ln.split()[0]: ln.split() for ln in r.stdout.splitlines() if ln.startswith("blk")}
+    assert lines["blk.0.ffn_down.weight"][3] == "Q4_1"
+    assert all(lines[f"blk.{i}.ffn_down.weight"][3] == "Q4_0" for i in range(1, 8))
+
+
+@pytest.mark.parametrize("scheme,want", [
+    ("Q4_K_M", {"attn_q": "Q5_0", "attn_v": "Q8_0", "ffn_down": "Q8_0"}),
+    ("Q5_K_S", {"attn_q": "Q5_1"}),
+    ("IQ4_XS", {"attn_q": "IQ4_NL"}),
+])
+def test_shape_fallback_types(tmp_path, scheme, want):
+    # tensor_type_fallback (scheme.py:364-384): k % 256 != 0 -> a 32-value block type
+    src = tmp_path / "in.gguf"
+    fallback_model(src)
+    r = run_cli(src, tmp_path / "o.gguf", scheme, "--dry-run")
+    lines = {ln.split()[0]: ln.split() for ln in r.stdout.splitlines() if ln.startswith("blk")}
+    for short, t in want.items():
+        assert lines[f"blk.0.{short}.weight"][3] == t, (short, lines[f"blk.0.{short}.weight"])
+    assert "falling back to" in r.stderr
