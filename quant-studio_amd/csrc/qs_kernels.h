@@ -245,12 +245,12 @@ __global__ __launch_bounds__(256) void k_b32(KArgs a) {
 // blocks of the final phase (L, out) are never live together (every kernel
 // passes several wave_syncs between them), so they share storage: less LDS
 // per workgroup, more resident waves.
-template <int SPW, int BYTES>
+template <int SPW, int BYTES, int VSB = SPW>
 struct alignas(16) SbLds {
     union {
         struct {
-            float v[SPW][QK_K];      // per-value staging for superblock sums
-            float tmp[SPW][40];
+            float v[VSB][QK_K];      // per-value staging for superblock sums (VSB at a time)
+            float tmp[VSB][40];
         };
         struct {
             uint8_t L[SPW][QK_K];
@@ -263,21 +263,52 @@ struct alignas(16) SbLds {
 };
 
 // finish: every valid superblock of the wave has its bytes in s.out
-template <int SPW, int BYTES>
-QS_DEV void sb_store(const SbLds<SPW, BYTES>& s, const KArgs& a) {
+template <int SPW, int BYTES, int VSB>
+QS_DEV void sb_store(const SbLds<SPW, BYTES, VSB>& s, const KArgs& a) {
     const int64_t first = (int64_t)blockIdx.x * SPW;
     const int64_t nvalid = min((int64_t)SPW, a.n_units - first);
     store_staged(s.out, a.dst, first * BYTES, (int)nvalid * BYTES);
+}
+
+// sb_cascade8_256 of x^2 over each superblock of the wave, staged half the
+// wave's superblocks at a time (half the LDS). Every lane takes part in both
+// rounds, the wave barriers included; lanes of the other half compute the
+// same sums from the same staged values and discard them.
+template <int LPS, int SPW>
+QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x)[32], int slot, int g) {
+    constexpr int H = SPW / 2;
+    const int hs = slot % H;
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const bool mine = slot / H == r;
+        if (mine) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[hs][32 * g + i] = x[i] * x[i];
+        }
+        wave_sync();
+        const float t = sb_cascade8_256<LPS>(v[hs], tmp[hs], g);
+        sum = mine ? t : sum;
+        wave_sync();                          // the next round restages v and tmp
+    }
+    return sum;
 }
 
 // ------------------------------------------------------------------
 // Q4_K / Q5_K  (q4_k.py:25-79, q5_k.py:25-82)
 // ------------------------------------------------------------------
 template <int SRC, bool IMAT, int NMAX>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_q45_k(KArgs a, Steps steps, QpSteps qps) {
+// Occupancy: the imatrix variant (143 VGPRs) runs 3 waves per SIMD; the other
+// (131) is held to 128 for a fourth wave: its 6 spilled registers cost one
+// scratch store on an accepted candidate and reloads after the candidate
+// loop (measured 5% faster). Held to 128, the imatrix variant spills inside
+// the loop and is 7% slower.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4))) void k_q45_k(KArgs a, Steps steps, QpSteps qps) {
     constexpr int LPS = 8, SPW = 8, BYTES = NMAX == 15 ? 144 : 176;
     constexpr float FMAX = (float)NMAX;
-    __shared__ SbLds<SPW, BYTES> s;
+    // the imatrix path stages x^2 of all 8 superblocks for sigma2; the other
+    // keeps no per-value staging (its weights need only the lane's own sum)
+    __shared__ SbLds<SPW, BYTES, IMAT ? SPW : 1> s;
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32];
@@ -679,7 +710,9 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
 template <int SRC, bool IMAT>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_xs(KArgs a) {
     constexpr int LPS = 8, SPW = 8, BYTES = 136;
-    __shared__ SbLds<SPW, BYTES> s;
+    // LDS is what limits this kernel's residency: the imatrix path stages x^2
+    // for sigma2 half the wave's superblocks at a time, the other stages none
+    __shared__ SbLds<SPW, BYTES, IMAT ? SPW / 2 : 1> s;
     __shared__ float2 iq4tab[256];
     __shared__ uint8_t iq4mu[256];
     iq4_build_table(iq4tab, iq4mu);
@@ -688,10 +721,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     float x[32], w[32];
     load_elems<SRC, true, 32>(a.src, p.elem, x);
     if constexpr (IMAT) {
-#pragma unroll
-        for (int i = 0; i < 32; i++) s.v[slot][32 * g + i] = x[i] * x[i];
-        wave_sync();
-        const float sigma2 = (2.0f * sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g)) / 256.0f;
+        const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW>(s.v, s.tmp, x, slot, g)) / 256.0f;
         imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
     } else {
 #pragma unroll
