@@ -40,14 +40,19 @@ constexpr int IQ2_CH = 8, IQ3_CH = 4;
 constexpr int IQ2_256_MAXCH = 19, IQ2_512_MAXCH = 37, IQ2_1024_MAXCH = 9;
 constexpr int IQ3_256_MAXCH = 9, IQ3_512_MAXCH = 10;
 
-// LDS of the IQ kernels: x^2 staging for the superblock sum, per-group
-// scales, and the packed output blocks.
+// LDS of the IQ kernels: x^2 staging for the superblock sum (half the wave's
+// superblocks at a time), sharing its storage with the packed output blocks
+// written at the end, and the per-group scales.
 template <int SPW, int BYTES>
 struct alignas(16) IqLds {
-    float v[SPW][QK_K];
-    float tmp[SPW][40];
+    union {                      // the weight phase's staging, then the packed blocks
+        struct {
+            float v[SPW / 2][QK_K];      // x^2 of half the wave's superblocks at a time
+            float tmp[SPW / 2][40];
+        };
+        uint8_t out[SPW * BYTES + 16];
+    };
     float sc[SPW][16];
-    uint8_t out[SPW * BYTES + 16];
 };
 
 template <int SPW, int BYTES>
@@ -351,18 +356,16 @@ struct IqSteps {
 };
 
 template <int SRC, int LPS, int GROUP>
-QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float* vlds, float* tmp, float sig_mult,
-                            bool use_x2, float (&x)[GROUP], float (&w)[GROUP]) {
+QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K], float (*tmp)[40],
+                            float sig_mult, bool use_x2, float (&x)[GROUP], float (&w)[GROUP]) {
+    constexpr int SPW = 64 / LPS;
     load_elems<SRC, true, GROUP>(a.src, p.elem, x);
     if (use_x2) {
 #pragma unroll
         for (int i = 0; i < GROUP; i++) w[i] = x[i] * x[i];
         return;
     }
-#pragma unroll
-    for (int i = 0; i < GROUP; i++) vlds[GROUP * p.g + i] = x[i] * x[i];
-    wave_sync();
-    const float sum = sb_cascade8_256<LPS>(vlds, tmp, p.g);
+    const float sum = sb_sumsq_halves<LPS, SPW, GROUP>(vlds, tmp, x, p.slot, p.g);
     const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
     imatrix_weights<GROUP>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
 }
@@ -381,7 +384,7 @@ __global__ __launch_bounds__(64) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
-    iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 1.0f, false, x, w);
+    iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 1.0f, false, x, w);
     sqrt_ref_n<32>(w, a.sqrt_down, waux);
     int signs[4];
     static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
@@ -487,7 +490,7 @@ __global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sw
     const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
-    iq_load_weights<SRC, LPS, 16>(a, p, s.v[slot], s.tmp[slot], IS_S ? 2.0f : 1.0f, false, x, w);
+    iq_load_weights<SRC, LPS, 16>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
     sqrt_ref_n<16>(w, a.sqrt_down, waux);
     int signs[2];
     if constexpr (IS_S) {
@@ -617,7 +620,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void k_
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
-    iq_load_weights<SRC, LPS, 32>(a, p, s.v[slot], s.tmp[slot], 2.0f, !IMAT, x, w);
+    iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
     sqrt_ref_n<32>(w, a.sqrt_down, waux);
     int signs[4];
     if constexpr (IS_S) {

@@ -274,8 +274,9 @@ QS_DEV void sb_store(const SbLds<SPW, BYTES, VSB>& s, const KArgs& a) {
 // wave's superblocks at a time (half the LDS). Every lane takes part in both
 // rounds, the wave barriers included; lanes of the other half compute the
 // same sums from the same staged values and discard them.
-template <int LPS, int SPW>
-QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x)[32], int slot, int g) {
+template <int LPS, int SPW, int GROUP>
+QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x)[GROUP], int slot, int g) {
+    static_assert(GROUP * LPS == QK_K, "the lanes of a superblock cover its values");
     constexpr int H = SPW / 2;
     const int hs = slot % H;
     float sum = 0.0f;
@@ -284,7 +285,7 @@ QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x
         const bool mine = slot / H == r;
         if (mine) {
 #pragma unroll
-            for (int i = 0; i < 32; i++) v[hs][32 * g + i] = x[i] * x[i];
+            for (int i = 0; i < GROUP; i++) v[hs][GROUP * g + i] = x[i] * x[i];
         }
         wave_sync();
         const float t = sb_cascade8_256<LPS>(v[hs], tmp[hs], g);
@@ -721,7 +722,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     float x[32], w[32];
     load_elems<SRC, true, 32>(a.src, p.elem, x);
     if constexpr (IMAT) {
-        const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW>(s.v, s.tmp, x, slot, g)) / 256.0f;
+        const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW, 32>(s.v, s.tmp, x, slot, g)) / 256.0f;
         imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
     } else {
 #pragma unroll
