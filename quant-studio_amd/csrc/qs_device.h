@@ -43,6 +43,16 @@ QS_DEV float rdiv(float c, float t) {
 }
 QS_DEV float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
+// Register-allocation hints (no instructions): the value is taken to change
+// here, so the compiler can neither recompute it later from its inputs (which
+// would keep those live instead) nor hoist work that uses it out of a loop.
+QS_DEV void keep_in_register(float& v) { asm volatile("" : "+v"(v)); }
+template <int N>
+QS_DEV void keep_in_registers(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; i++) keep_in_register(v[i]);
+}
+
 // The reference's square root (torch.sqrt on CPU, kernels/q4_k.py:34, :51,
 // iq2.py:431, :436 and the other weight sites): the IEEE root, one ulp lower
 // when the input's key (exponent parity << 23 | mantissa, subnormals scaled

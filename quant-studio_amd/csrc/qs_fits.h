@@ -173,7 +173,7 @@ QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const fl
             float wi = w[i];
             // keeps wi * xi inside the pass: hoisting the N products out of
             // the loop would hold N more registers for the whole fit
-            asm volatile("" : "+v"(wi));
+            keep_in_register(wi);
             const float slx = sumlx - (wi * xi) * Li;
             const float sl2 = suml2 - (wi * Li) * Li;
             const bool ok = slx > 0 && sl2 > 0;
