@@ -155,3 +155,26 @@ def test_empty_and_single_row(qs, dev):
     x, qw = c2_like(1, 256, seed=3)
     got = hip_quantize(qs, "q4_k", x, qw, dev)
     assert np.array_equal(got, oracle.quantize("q4_k", x, qw))
+
+
+def test_iq2_xxs_full_ffn_down_tensor_heavy_tailed(qs, dev):
+    """BASELINE IQ2_XXS workload at full size: one 2560x9728 ffn_down tensor of
+    Student-t (df 5) weights scaled to std 0.02 with a log-normal imatrix.
+    Every row is quantized on the GPU; 64 rows spread over the tensor are
+    compared with the oracle byte for byte, and the whole tensor's
+    dequantized error stays at the format's level."""
+    import dequant
+    rng = np.random.default_rng(44)
+    rows, k = 2560, 9728
+    a = rng.standard_t(5, size=(rows, k)) * (0.02 / np.sqrt(5 / 3))
+    x = bf16_bits(a)
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    got = hip_quantize(qs, "iq2_xxs", x, qw, dev)
+    sel = np.linspace(0, rows - 1, 64).astype(int)
+    ref = oracle.quantize("iq2_xxs", x[sel], qw, n_threads=NTHREADS)
+    same = block_identical(got[sel], ref, "iq2_xxs")
+    assert same.all(), f"{int((~same).sum())}/{same.size} blocks differ"
+    xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xh = dequant.dequantize("iq2_xxs", got, rows)
+    rel = np.sqrt(((xf - xh) ** 2).mean() / (xf ** 2).mean())
+    assert rel < 0.62, rel
