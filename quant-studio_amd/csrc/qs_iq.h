@@ -482,7 +482,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 // iq2_xs.py:20-69; quantize_iq2_s iq2_s.py:21-62
 // ------------------------------------------------------------------
 template <int SRC, bool IS_S>
-__global__ __launch_bounds__(64) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
+// IQ2_XS fits 4 waves per SIMD in 128 VGPRs without spills (8% faster than
+// 3); IQ2_S is held to 3 by its LDS (the 1024-entry grid) and spills at 128
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4))) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
     constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 82 : 74, GS = IS_S ? 1024 : 512;
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ __align__(16) uint32_t glds[GS * 2];
