@@ -13,6 +13,20 @@ namespace qs {
 // between lanes.
 QS_DEV void wave_sync() { __syncthreads(); }
 
+// Inclusive prefix sum of x over the wave's 64 lanes, in VALU only: DPP row
+// shifts 1, 2, 4, 8 scan each row of 16 lanes, then row broadcasts carry lane
+// 15's and lane 31's totals into the rows above (no LDS round trips).
+QS_DEV int wave_incl_scan(int x) {
+    int v = x;
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15 -> rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31 -> rows 2, 3
+    return v;
+}
+
 // Superblock position of this lane.
 struct SbPos {
     int64_t sb;      // global superblock index (clamped copy used for loads)
