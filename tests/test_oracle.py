@@ -178,3 +178,43 @@ def test_golden_vectors_catch_planted_mistake(mut):
             assert caught, f"planted mistake '{what}' not detected by {qtype} golden vectors"
     finally:
         L.qso_set_mutation(0)
+
+
+def _sqrt_down_keys() -> np.ndarray:
+    """The map's keys (parity << 23 | mantissa), from the generated header."""
+    import re
+    from pathlib import Path
+    txt = (Path(__file__).resolve().parents[1] / "quant-studio_amd" / "csrc" / "qs_sqrt_table.h").read_text()
+    gaps = np.array([int(v) for v in re.findall(r"\d+", txt[txt.index("{") + 1: txt.rindex("}")])], np.int64)
+    return np.cumsum(gaps)
+
+
+def _near_midpoint(v: np.ndarray) -> np.ndarray:
+    """sqrt_near_midpoint of qs_device.h, op for op in float32: the remainder
+    v - r^2 (exact, as the kernels' fma gives it) against -0.875 r ulp(r)."""
+    r = np.sqrt(v)
+    rem64 = v.astype(np.float64) - r.astype(np.float64) ** 2
+    rem = rem64.astype(np.float32)
+    ulp = (((r.view(np.uint32) & np.uint32(0x7f800000)) - np.uint32(23 << 23))).view(np.float32)
+    lim = (np.float32(-0.875) * r) * ulp
+    return (rem < lim) | (v.view(np.uint32) < np.uint32(0x17800000)), rem64, rem
+
+
+def test_sqrt_map_is_read_for_every_listed_input():
+    """The kernels read the square-root map only for inputs whose root lies
+    within 1/16 ulp of the midpoint below the IEEE root: every one of the 2^24
+    key classes in [1, 4) that the map lists passes that test, also scaled by
+    powers of 4 down to the tiny-input cutoff and up to the largest floats, and
+    about 6% of all inputs do."""
+    keys = _sqrt_down_keys()
+    m = np.arange(1 << 23, dtype=np.uint32)
+    x = np.concatenate([(127 << 23) | m, (128 << 23) | m]).astype(np.uint32).view(np.float32)
+    near, rem64, rem = _near_midpoint(x)
+    assert np.array_equal(rem.astype(np.float64), rem64)        # the remainder is exact in f32
+    assert near[keys].all()
+    assert 0.061 < near.mean() < 0.064
+    xd = x[keys]
+    for k in (-45, -41, -40, -20, -3, -1, 1, 7, 30, 62):
+        xs = (xd.astype(np.float64) * 4.0 ** k).astype(np.float32)
+        assert np.isfinite(xs).all() and (xs > 0).all()
+        assert _near_midpoint(xs)[0].all(), k
