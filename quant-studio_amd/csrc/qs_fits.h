@@ -56,10 +56,17 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
     }
     float best = tree_sum(t);
 
+    // 16-value groups load each step one candidate ahead, so the scalar
+    // load's latency is not waited for at the top of every candidate (Q2_K
+    // 2-6% faster); the 32-value loop measured 0-1.4% slower that way
+    constexpr bool AHEAD = N == 16;
+    float step_next = steps.v[0];
 #pragma unroll 1
     for (int s = 0; s < steps.n; s++) {
+        const float step = AHEAD ? step_next : steps.v[s];
+        if constexpr (AHEAD) step_next = steps.v[s + 1 < 40 ? s + 1 : 39];
         den = degen ? 1.0f : mx - mn;
-        const float isc = steps.v[s] / den;
+        const float isc = step / den;
         // the three tree sums are formed 8 values at a time (the tree over N
         // is the trees over its 8-value blocks, then the tree over the block
         // sums), so only one block of products is live at once
@@ -221,9 +228,12 @@ QS_DEV QxResult qx_fit(const float (&x)[N], const float (&w)[N], int nmax, const
     const float sumlx = seq_sum(t), suml2 = seq_sum(u);
     float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx, best_isc = iscale;
+    float step_next = steps.v[0];      // loaded one candidate ahead (Q3_K 4%, Q6_K 2% faster)
 #pragma unroll 1
     for (int s = 0; s < steps.n; s++) {
-        const float isc = rdiv(-steps.v[s], mxs);
+        const float step = step_next;
+        step_next = steps.v[s + 1 < 40 ? s + 1 : 39];
+        const float isc = rdiv(-step, mxs);
 #pragma unroll
         for (int i = 0; i < N; i++) {
             float La = clampf(rintf(isc * x[i]), -fmax, fmax - 1.0f);
