@@ -165,19 +165,39 @@ def identical_pct(torch, qs, oracle, qtype, imat, host, qws, rows=256):
     return 100.0 * same / total
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(oracle, host, qws):
-    """The oracle on the full headline workload (Q4_K + imatrix), all host cores."""
+    """The oracle on the full headline workload (Q4_K + imatrix), all host
+    cores; plus one thread on the first eighth of each tensor's rows."""
     cores = len(os.sched_getaffinity(0))
-    n = 0
-    t0 = time.perf_counter()
-    for j in range(len(SHAPES)):
-        x = host[j].float().numpy()
-        oracle.quantize("q4_k", x, qws[j].cpu().numpy(), n_threads=cores)
-        n += x.size
-    dt = time.perf_counter() - t0
+
+    def run(rows_frac, threads):
+        n = 0
+        t0 = time.perf_counter()
+        for j in range(len(SHAPES)):
+            x = host[j][: max(1, SHAPES[j][0] // rows_frac)].float().numpy()
+            oracle.quantize("q4_k", x, qws[j].cpu().numpy(), n_threads=threads)
+            n += x.size
+        return n, time.perf_counter() - t0
+
+    n, dt = run(1, cores)
+    n1, dt1 = run(8, 1)
     return {"value": round(2 * n / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+            "value_1_thread": round(2 * n1 / dt1 / 1e9, 5), "cpu": cpu_model(),
             "sample": f"full workload: Q4_K+imatrix on bf16 {SHAPES[0][0]}x{SHAPES[0][1]} and "
-                      f"{SHAPES[1][0]}x{SHAPES[1][1]} ({n} values), {dt:.2f} s, one pass"}
+                      f"{SHAPES[1][0]}x{SHAPES[1][1]} ({n} values), {dt:.2f} s, one pass; "
+                      f"1 thread: the first 1/8 of each tensor's rows ({n1} values), {dt1:.2f} s"}
 
 
 def q4_0_large(torch, qs, dev, steps: int) -> dict:
