@@ -90,6 +90,8 @@ int64_t qs_row_bytes(int ggml_type, int64_t k);
  *   dst:           device pointer receiving n_rows * qs_row_bytes(k) bytes;
  *                  dst_bytes must be at least that
  *   hip_stream:    hipStream_t to launch on (NULL = null stream)
+ * At most 2^34 values (n_rows * k) per call, and n_rows * src_row_stride_bytes
+ * below 2^62; larger calls are refused with QS_EINVAL (split them by rows).
  * Asynchronous and stream-ordered; allocates nothing. The output bytes do not
  * depend on how rows are split across calls. */
 int qs_quantize(int ggml_type, int src_type, const void *src, int64_t n_rows, int64_t k,
@@ -126,8 +128,9 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline 
  * (rows contiguous), quantized to ggml_type in chunks of rows_per_chunk rows
  * with the host imatrix (k floats or NULL; as qs_quantize), the output rows
  * written contiguously at out_offset of fd. Returns once every chunk is
- * queued; blocks only while all slots are busy. One pipeline.quantize_tensor
- * call of the reference (quant-studio.py:180-213, driven from :453-461). */
+ * queued; blocks only while all slots are busy. At most 2^34 values per
+ * tensor (QS_EINVAL otherwise). One pipeline.quantize_tensor call of the
+ * reference (quant-studio.py:180-213, driven from :453-461). */
 int qs_pipeline_quantize(qs_pipeline *p, int ggml_type, int src_type, const void *src,
                          int64_t n_rows, int64_t k, const float *imatrix,
                          int64_t rows_per_chunk, int fd, int64_t out_offset);

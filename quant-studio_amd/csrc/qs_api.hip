@@ -418,12 +418,22 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     if (k <= 0 || k % t->blk)
         return fail(QS_EINVAL, "%s: row length %lld is not a positive multiple of %d", t->name,
                     (long long)k, t->blk);
+    // size limits, checked by division so no product below can wrap: at most
+    // 2^34 values per call (64 GiB of f32; every launch's grid then stays
+    // below 2^32 work-items) and a source span below 2^62 bytes
+    constexpr int64_t kMaxValues = INT64_C(1) << 34, kMaxSpan = INT64_C(1) << 62;
+    if (k > kMaxValues || n_rows > kMaxValues / k)
+        return fail(QS_EINVAL, "%lld x %lld values exceed the 2^34 per call", (long long)n_rows,
+                    (long long)k);
     const int64_t rb = k / t->blk * t->bytes;
     if (n_rows == 0) return 0;
     if (!src || !dst) return fail(QS_EINVAL, "null src or dst");
     if (src_row_stride_bytes < k * esz || src_row_stride_bytes % 16)
         return fail(QS_EINVAL, "row stride %lld must be >= %lld and a multiple of 16",
                     (long long)src_row_stride_bytes, (long long)(k * esz));
+    if (n_rows > kMaxSpan / src_row_stride_bytes)
+        return fail(QS_EINVAL, "%lld rows of stride %lld bytes exceed a 2^62-byte span",
+                    (long long)n_rows, (long long)src_row_stride_bytes);
     if (reinterpret_cast<uintptr_t>(src) % 16) return fail(QS_EINVAL, "src must be 16-byte aligned");
     if (dst_bytes < n_rows * rb)
         return fail(QS_EINVAL, "dst holds %lld bytes, %lld needed", (long long)dst_bytes,

@@ -313,6 +313,12 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
     if (!qs_type_supported(ggml_type)) return fail(QS_ENOTSUP, "ggml type %d has no HIP quantizer", ggml_type);
     const int64_t out_row = qs_row_bytes(ggml_type, k);
     if (out_row < 0) return (int)out_row;
+    // the same per-call limit as qs_quantize (2^34 values), checked before any
+    // chunk size is formed from n_rows * k
+    constexpr int64_t kMaxValues = INT64_C(1) << 34;
+    if (k > kMaxValues || n_rows > kMaxValues / k)
+        return fail(QS_EINVAL, "%lld x %lld values exceed the 2^34 per tensor", (long long)n_rows,
+                    (long long)k);
     if (n_rows == 0) return 0;
     if (!src) return fail(QS_EINVAL, "null src");
     if (qs_type_needs_imatrix(ggml_type) == 1 && !imatrix)

@@ -82,6 +82,12 @@ def test_quantize_rejects_bad_arguments_before_launch(qs):
     assert _call(L, 12, dst_bytes=10) == -22         # dst too small
     assert b"dst holds 10 bytes" in L.qs_last_error()
     assert _call(L, 12, n=0) == 0                    # empty input: no work, no launch
+    # sizes whose products would wrap int64 are refused before any arithmetic
+    assert _call(L, 12, n=1 << 40, k=1 << 20) == -22
+    assert b"exceed the 2^34" in L.qs_last_error()
+    assert _call(L, 12, n=1 << 20, k=1 << 14, stride=1 << 50) == -22
+    assert b"2^62-byte span" in L.qs_last_error()
+    assert _call(L, 12, n=(1 << 34) // 256 + 1, k=256, stride=512) == -22
 
 
 def test_needs_imatrix_types_reject_missing_imatrix(qs):

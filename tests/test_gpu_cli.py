@@ -137,3 +137,21 @@ def test_shape_fallback_types_end_to_end(tmp_path, scheme, ftype):
     types = {int(t.ggml_type) for t in io.GGUFReader(out).tensors}
     assert types & {int(GT.Q5_0), int(GT.Q5_1), int(GT.Q8_0), int(GT.IQ4_NL)}
     check_output(src, out, expect, ftype=ftype, imatrix=io.load_imatrix(im))
+
+
+def test_pipeline_refuses_sizes_that_would_wrap(tmp_path):
+    """A tensor of more than 2^34 values is refused before any chunk size is
+    formed from n_rows * k (those products could wrap int64)."""
+    import ctypes
+    import os
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    fd = os.open(tmp_path / "o.bin", os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        with pl.NativePipeline(0, fd) as p:
+            rc = p.L.qs_pipeline_quantize(p.h, 12, 30, ctypes.c_void_p(16), 1 << 40, 1 << 20, None,
+                                          1, fd, 0)
+            assert rc == -22 and "exceed the 2^34" in qs.last_error()
+            p.finish()
+    finally:
+        os.close(fd)
