@@ -124,6 +124,9 @@ def row_bytes(ggml_type: int, k: int) -> int:
     return rb
 
 
+MAX_VALUES_PER_CALL = 1 << 34      # qs_quantize's per-call limit (include/quant_studio.h)
+
+
 def quantize(ggml_type: int, x, qw, out=None):
     """Quantize the rows of x (n, k) on its ROCm device; returns uint8 (n, row_bytes).
 
@@ -154,10 +157,16 @@ def quantize(ggml_type: int, x, qw, out=None):
         qptr = qw.data_ptr()
     stride_bytes = (x.stride(0) if n > 1 else k) * x.element_size()
     stream = torch.cuda.current_stream(x.device).cuda_stream
-    rc = library().qs_quantize(int(ggml_type), src_id, x.data_ptr(), n, k,
-                               stride_bytes, qptr, out.data_ptr(), out.numel(), stream)
-    if rc != 0:
-        raise QuantSpecError(last_error())
+    # one C call takes at most MAX_VALUES_PER_CALL values: larger inputs go in
+    # row ranges (the bytes do not depend on the split)
+    rows = max(1, MAX_VALUES_PER_CALL // max(k, 1))
+    for r0 in range(0, max(n, 1), rows):
+        m = max(0, min(rows, n - r0))
+        rc = library().qs_quantize(int(ggml_type), src_id, x.data_ptr() + r0 * stride_bytes, m, k,
+                                   stride_bytes, qptr, out.data_ptr() + r0 * rb,
+                                   out.numel() - r0 * rb, stream)
+        if rc != 0:
+            raise QuantSpecError(last_error())
     return out.view(n, rb) if out.dim() != 2 else out
 
 

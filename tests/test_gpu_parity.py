@@ -178,3 +178,20 @@ def test_iq2_xxs_full_ffn_down_tensor_heavy_tailed(qs, dev):
     xh = dequant.dequantize("iq2_xxs", got, rows)
     rel = np.sqrt(((xf - xh) ** 2).mean() / (xf ** 2).mean())
     assert rel < 0.62, rel
+
+
+def test_python_mirror_splits_calls_over_the_value_limit(dev, monkeypatch):
+    """quant_fn inputs above the C call's value limit go in row ranges with the
+    same bytes as one call (limit lowered here to 3 rows, 7 rows in all)."""
+    import importlib
+    qs = importlib.import_module("quant-studio_amd")
+    rng = np.random.default_rng(21)
+    x = (rng.normal(size=(7, 512)) * 0.02).astype(np.float32)
+    qw = rng.lognormal(size=512).astype(np.float32)
+    for qtype in ("q4_k", "iq2_xs"):
+        whole = hip_quantize(qs, qtype, x, qw, dev)
+        monkeypatch.setattr(qs, "MAX_VALUES_PER_CALL", 3 * 512)
+        split = hip_quantize(qs, qtype, x, qw, dev)
+        monkeypatch.undo()
+        assert np.array_equal(whole, split), qtype
+        assert np.array_equal(whole, oracle.quantize(qtype, x, qw, n_threads=NTHREADS)), qtype
