@@ -158,22 +158,29 @@ template <int BITS, int NV, int CH>
 QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&wd)[CH / 2], int kc, int o_n,
                                         float o_sc, const float (&xs)[NV], const float (&ws)[NV]) {
     unsigned long long best = ~0ull;
+    // every slot's grid levels are read from LDS before any is used, so the
+    // chunk waits for LDS once instead of once per slot
+    int gi[CH];
+    Levels<NV> gl[CH];
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        gi[j] = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+        gl[j] = grid_levels<NV>(glds, gi[j]);
+    }
 #pragma unroll
     for (int j = 0; j < CH; j++) {
         const int pos = CH * kc + j;
-        const int gi = (int)((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-        const Levels<NV> gl = grid_levels<NV>(glds, gi);
         float d2 = 0.0f;
 #pragma unroll
         for (int e = 0; e < NV; e++) {
-            float diff = o_sc * level<NV>(gl, e);
+            float diff = o_sc * level<NV>(gl[j], e);
             diff = diff - xs[e];
             const float t = (ws[e] * diff) * diff;
             if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
             else d2 = d2 + t;
         }
         const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
-                                       ((unsigned long long)pos << 16) | (unsigned)gi;
+                                       ((unsigned long long)pos << 16) | (unsigned)gi[j];
         best = (pos < o_n && key < best) ? key : best;
     }
     return best;
