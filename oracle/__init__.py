@@ -2,8 +2,8 @@
 
 A plain-C restatement of the reference's eager CPU path (kernels/*.py under
 torch on CPU), loaded with ctypes. Only tests/, __graft_entry__.smoke() and the
-CPU-baseline leg of bench.py use it, always as the checker or the timed CPU
-baseline; the product library never calls it.
+CPU-baseline leg of bench.py use it, always as the expected result to compare
+against or as the timed CPU baseline; the product library never calls it.
 
 Parity pinning: every type is checked against golden vectors written by the
 reference itself (tests/golden/gen_golden.py); the reduction-order helpers and

@@ -1,6 +1,6 @@
 """GPU end to end at full size: the command line on the synthetic 4B-class
 bf16 model (36 layers, hidden 2560, ffn 9728, vocab 151936, tied embeddings,
-per-tensor log-normal imatrix), for the BASELINE model runs: Q4_K_M, IQ2_XXS,
+per-tensor log-normal imatrix), for the whole-model schemes: Q4_K_M, IQ2_XXS,
 and IQ3_XXS / IQ2_S with a Q4_0 token embedding. Each run's output must hold
 every tensor of the plan (`--dry-run`) with its type and size, passthroughs
 unchanged, and for every quantized tensor three rows (first, middle, last)

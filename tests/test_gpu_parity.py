@@ -83,7 +83,7 @@ def test_oracle_parity_random(qs, dev, qtype, imat):
 
 
 def test_q4_0_full_4096x4096(qs, dev):
-    """BASELINE config: Q4_0 on one bf16 4096x4096 tensor, N(0, 0.02) with 0.1%
+    """Q4_0 on one bf16 4096x4096 tensor, N(0, 0.02) with 0.1%
     outliers x20, seed 0, byte-exact."""
     rng = np.random.default_rng(0)
     a = rng.normal(0.0, 0.02, (4096, 4096))
@@ -97,7 +97,7 @@ def test_q4_0_full_4096x4096(qs, dev):
 
 
 def test_q4_k_imatrix_full_ffn_shapes(qs, dev):
-    """BASELINE config: Q4_K with imatrix on 9728x2560 and 2560x9728 bf16,
+    """Q4_K with imatrix on the ffn shapes 9728x2560 and 2560x9728 bf16,
     per-row log-normal std jitter, log-normal per-column imatrix."""
     for rows, k, seed in ((9728, 2560, 1), (2560, 9728, 2)):
         print(f"q4_k imat {rows}x{k}", flush=True)
@@ -158,7 +158,7 @@ def test_empty_and_single_row(qs, dev):
 
 
 def test_iq2_xxs_full_ffn_down_tensor_heavy_tailed(qs, dev):
-    """BASELINE IQ2_XXS workload at full size: one 2560x9728 ffn_down tensor of
+    """IQ2_XXS at full size: one 2560x9728 ffn_down tensor of
     Student-t (df 5) weights scaled to std 0.02 with a log-normal imatrix.
     Every row is quantized on the GPU; 64 rows spread over the tensor are
     compared with the oracle byte for byte, and the whole tensor's
