@@ -153,11 +153,17 @@ QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_
 // First minimum of one chunk (CH list slots from slot CH*kc) as a 64-bit key
 // (distance bits, list position, grid index); slots past the list end (o_n)
 // are masked out. Every slot is evaluated (padding holds index 0, a valid
-// grid point), without branches.
+// grid point), without branches. IQ2: slots are visited in list order, so a
+// strict `d2 < best` keeps the first minimum and the key is built once per
+// chunk (4-7% faster); a chunk with no finite distance returns ~0 (as if it
+// held no candidate: the search's result is then -1 either way). IQ3 compares
+// the 64-bit key per slot (its 4-slot chunks measured 1-2% faster that way).
 template <int BITS, int NV, int CH>
 QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&wd)[CH / 2], int kc, int o_n,
                                         float o_sc, const float (&xs)[NV], const float (&ws)[NV]) {
-    unsigned long long best = ~0ull;
+    unsigned long long best = ~0ull;     // IQ3
+    float best_d2 = __builtin_inff();    // IQ2
+    int best_j = -1;
     // every slot's grid levels are read from LDS before any is used, so the
     // chunk waits for LDS once instead of once per slot
     int gi[CH];
@@ -179,11 +185,23 @@ QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&w
             if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
             else d2 = d2 + t;
         }
-        const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
-                                       ((unsigned long long)pos << 16) | (unsigned)gi[j];
-        best = (pos < o_n && key < best) ? key : best;
+        if constexpr (BITS == 3) {
+            const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
+                                           ((unsigned long long)pos << 16) | (unsigned)gi[j];
+            best = (pos < o_n && key < best) ? key : best;
+        } else {
+            const bool take = pos < o_n && d2 < best_d2;
+            best_d2 = take ? d2 : best_d2;
+            best_j = take ? j : best_j;
+        }
     }
-    return best;
+    if constexpr (BITS == 3) return best;
+    if (best_j < 0) return ~0ull;
+    int best_gi = gi[0];
+#pragma unroll
+    for (int j = 1; j < CH; j++) best_gi = best_j == j ? gi[j] : best_gi;
+    return ((unsigned long long)__float_as_uint(best_d2) << 32) |
+           ((unsigned long long)(CH * kc + best_j) << 16) | (unsigned)best_gi;
 }
 
 template <int CH>
