@@ -181,9 +181,11 @@ QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&w
         for (int e = 0; e < NV; e++) {
             float diff = o_sc * level<NV>(gl[j], e);
             diff = diff - xs[e];
+            // IQ2's sum runs from +0 (iq2.py) and IQ3's from its first term;
+            // t = (w*d)*d is never -0 (the two factors d carry the same
+            // sign), so +0 + t0 == t0 and both start from the first term
             const float t = (ws[e] * diff) * diff;
-            if constexpr (BITS == 3) d2 = (e == 0) ? t : d2 + t;
-            else d2 = d2 + t;
+            d2 = (e == 0) ? t : d2 + t;
         }
         if constexpr (BITS == 3) {
             const unsigned long long key = ((unsigned long long)__float_as_uint(d2) << 32) |
