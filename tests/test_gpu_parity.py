@@ -69,15 +69,18 @@ def c2_like(rows: int, k: int, seed: int):
 @pytest.mark.parametrize("qtype", HIP_TYPES)
 @pytest.mark.parametrize("imat", [False, True])
 def test_oracle_parity_random(qs, dev, qtype, imat):
-    if qtype == "q4_0" and imat:
-        pytest.skip("Q4_0 ignores an imatrix")
-    if qtype in NEEDS_IMATRIX and not imat:
-        pytest.skip(f"{qtype} requires an imatrix")
+    """Random ffn-like rows against the oracle; Q4_0 ignores an imatrix (the
+    reference's Q4_0, q4_0.py:36-37) and the imatrix-only types refuse to run
+    without one (QuantSpec.needs_imatrix)."""
     x, qw = c2_like(384, 2560, seed=sum(map(ord, qtype)) * 2 + int(imat))
     qw = qw if imat else None
     print(f"{qtype} imat={imat} 384x2560", flush=True)
+    if qtype in NEEDS_IMATRIX and not imat:
+        with pytest.raises(qs.QuantSpecError, match="requires an imatrix"):
+            hip_quantize(qs, qtype, x, None, dev)
+        return
     got = hip_quantize(qs, qtype, x, qw, dev)
-    ref = oracle.quantize(qtype, x, qw, n_threads=NTHREADS)
+    ref = oracle.quantize(qtype, x, None if qtype == "q4_0" else qw, n_threads=NTHREADS)
     same = block_identical(got, ref, qtype)
     assert same.all(), f"{int((~same).sum())}/{same.size} blocks differ"
 
