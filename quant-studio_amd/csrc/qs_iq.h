@@ -236,20 +236,9 @@ QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, uns
     if (FIRST && n > 0) iq_load_chunk<CH>(T, (ci >> 12) & 0x7ffffu, own);
     const int nch = (n + CH - 1) / CH;
     const int nd = nch > FIRST ? nch - FIRST : 0;
-    // exclusive prefix sum of the lanes' dealt chunk counts. IQ3's lists are
-    // short, so its passes are dominated by this scan: there the DPP scan
-    // (VALU only) is 5-8% faster; for IQ2 the shuffle scan keeps the register
-    // allocation that measured 2-4% faster.
-    int incl = nd;
-    if constexpr (BITS == 3) {
-        incl = wave_incl_scan(nd);
-    } else {
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-            const int t = __shfl_up(incl, d);
-            if (lane >= d) incl += t;
-        }
-    }
+    // exclusive prefix sum of the lanes' dealt chunk counts, a DPP scan (VALU
+    // only; against a shuffle scan: IQ3 5-8%, IQ2_XXS 5%, IQ2_S 2% faster)
+    const int incl = wave_incl_scan(nd);
     const int excl = incl - nd;
     // the wave's dealt chunk count, read from lane 63 into a scalar register
     // so the round loop is scalar-controlled
