@@ -4,16 +4,28 @@
 Headline workload: Q4_K with an imatrix on the two ffn-shaped bf16 tensors
 9728x2560 and 2560x9728 (weights N(0, 0.02) with log-normal per-row std
 jitter, sigma 0.3; per-column log-normal imatrix). One step = one quantization
-pass over both tensors, inputs already resident in HBM; the buffers rotate over
->= 1 GiB of distinct copies so the 256 MB MALL cannot serve them.
+pass over both tensors (two launches), inputs already resident in HBM; the
+buffers rotate over >= 1 GiB of distinct copies so the 256 MB MALL cannot
+serve them. The GPU's clocks ramp up over the first ~100 launches, so the
+default warm-up is long enough to reach them; every launch of the timed steps
+is bracketed by HIP events on its stream, so the per-launch kernel time and
+the step time come from the same launches.
 
-The JSON line also carries, per quant type (same shapes, with and without
-imatrix), the kernel GB/s, its HBM-roofline fraction and the identical-block
-percentage against the CPU oracle on a row sample; plus the CPU baseline (the
-oracle, a C restatement of the reference's eager CPU path, timed on this host's
-cores on the full headline workload).
+The JSON line also carries:
+  - per_type: every HIP type with and without imatrix on the same shapes:
+    kernel GB/s, HBM-roofline fraction and VALU fraction;
+  - configs: Q4_0 on one 4096x4096 bf16 tensor with 0.1% outliers (seed 0),
+    and IQ2_XXS + imatrix on 36 heavy-tailed (Student-t, df 5) 2560x9728
+    ffn_down tensors, each timed as its own workload;
+  - cpu_baseline: the oracle (a C restatement of the reference's eager CPU
+    path) on this host's cores: the full headline workload timed, and per
+    type the full tensors, whose bytes also give each type's identical-block
+    percentage against the GPU, with the weighted-MSE tie rule applied to
+    every block that differs.
 
-usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--types all|none|q4_k,...]
+usage: python bench.py [--gpus 1] [--steps 100] [--warmup 300] [--types all|none|q4_k,...]
+       python bench.py --e2e 'IQ2_XXS;Q4_K_M'   the command line end to end on a
+                                               synthetic 4B-class model (warm and cold)
 """
 
 from __future__ import annotations
@@ -40,9 +52,19 @@ TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 1
             "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
 NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
 IGNORE_IMATRIX = {"q4_0", "q4_1", "q5_0", "q5_1", "q8_0"}
-BLOCK_BYTES = {t: (b // 8 if t in IGNORE_IMATRIX | {"iq4_nl"} else b) for t, b in OUT_BYTES_PER_256.items()}
+BLOCK_VALUES = {t: (32 if t in IGNORE_IMATRIX | {"iq4_nl"} else 256) for t in OUT_BYTES_PER_256}
+BLOCK_BYTES = {t: OUT_BYTES_PER_256[t] * BLOCK_VALUES[t] // 256 for t in OUT_BYTES_PER_256}
 SHAPES = [(9728, 2560), (2560, 9728)]   # (rows, k)
 ROTATE_BYTES = 1 << 30
+
+
+def modes_of(qtype: str) -> tuple:
+    return (False,) if qtype in IGNORE_IMATRIX else (True,) if qtype in NEEDS_IMATRIX else (False, True)
+
+
+def bf16_from(torch, a):
+    """float32 numpy array -> bf16 torch tensor (round to nearest even)."""
+    return torch.from_numpy(a.astype("float32", copy=False)).to(torch.bfloat16)
 
 
 def make_inputs(torch, dev, seed: int = 0):
@@ -53,22 +75,20 @@ def make_inputs(torch, dev, seed: int = 0):
     for rows, k in SHAPES:
         a = rng.standard_normal((rows, k), dtype=np.float32) * np.float32(0.02)
         a *= np.exp(np.float32(0.3) * rng.standard_normal((rows, 1), dtype=np.float32))
-        t = torch.from_numpy(a).to(torch.bfloat16)
+        t = bf16_from(torch, a)
         host.append(t)
         xs.append(t.to(dev))
         qws.append(torch.from_numpy(rng.lognormal(0.0, 1.0, k).astype(np.float32)).to(dev))
     return xs, qws, host
 
 
-def profiled(key: str) -> int | None:
-    """A per-launch figure of the headline kernel from the rocprofv3 counter runs
-    summarised in profiles/: HBM bytes (FETCH_SIZE + WRITE_SIZE, scaled by a copy
-    of known size) or VALU wave instructions (SQ_INSTS_VALU)."""
-    f = ROOT / "profiles" / "counters_q4_k_imat_9728x2560.md"
+def profile_figure(name: str, key: str) -> float | None:
+    """A figure recorded by a rocprofv3 summary in profiles/ (lines `key: value`)."""
+    f = ROOT / "profiles" / name
     if f.exists():
         for ln in f.read_text().splitlines():
             if ln.startswith(key + ":"):
-                return int(ln.split(":")[1])
+                return float(ln.split(":", 1)[1])
     return None
 
 
@@ -110,59 +130,48 @@ def valu_peak(torch, dev, launches: int = 5) -> float:
 
 
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
+    """bf16 in + packed blocks out + the imatrix (4k bytes)."""
     return 2 * n_elems + n_elems * OUT_BYTES_PER_256[qtype] // 256 + 4 * k
 
 
-def time_type(torch, qs, qtype, imat, xs_rot, qws, outs, steps, warmup):
-    """Returns (ms per step, per-shape average kernel ms) for one type."""
-    tid = TYPE_IDS[qtype]
-    nrot = len(xs_rot)
+def time_steps(torch, launches, steps: int, warmup: int):
+    """Run `warmup` untimed steps, then time exactly `steps` steps, a step being
+    the callables in `launches` (each queues one kernel; called with the step
+    index). Returns (wall ms per step, mean kernel ms per launch slot): an event
+    is recorded on the launch stream before the first and after every launch,
+    so consecutive events bracket one kernel each."""
     stream = torch.cuda.current_stream()
-
-    def step(i):
-        xs = xs_rot[i % nrot]
-        for j, x in enumerate(xs):
-            qs.quantize(tid, x, qws[j] if imat else None, out=outs[j])
-
     for i in range(warmup):
-        step(i)
+        for f in launches:
+            f(i)
     torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
+          for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        step(i)
+        ev[i][0].record(stream)
+        for j, f in enumerate(launches):
+            f(i)
+            ev[i][j + 1].record(stream)
     torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / steps
-    # per-launch kernel durations from HIP events on the launch stream: each
-    # shape's launches back to back between one pair of events, so the host's
-    # launch overhead (~8 us per call) overlaps the queued kernels instead of
-    # being counted in short ones
-    kms = []
-    for j, _ in enumerate(SHAPES):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(steps):
-            qs.quantize(tid, xs_rot[i % nrot][j], qws[j] if imat else None, out=outs[j])
-        b.record(stream)
-        torch.cuda.synchronize()
-        kms.append(a.elapsed_time(b) / steps)
-    return ms_step, kms
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per = [sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) / steps
+           for j in range(len(launches))]
+    return wall_ms, per
 
 
-def identical_pct(torch, qs, oracle, qtype, imat, host, qws, rows=256):
-    import numpy as np
-    same = total = 0
-    for j, (r, k) in enumerate(SHAPES):
-        xb = host[j][:rows]
-        qw = qws[j].cpu().numpy() if imat else None
-        got = qs.quantize(TYPE_IDS[qtype], xb.to(qws[j].device), qws[j] if imat else None)
-        got = got.cpu().numpy()
-        ref = oracle.quantize(qtype, xb.float().numpy(), qw,
-                              n_threads=len(os.sched_getaffinity(0)))
-        bb = BLOCK_BYTES[qtype]
-        a, b = got.reshape(-1, bb), ref.reshape(-1, bb)
-        same += int((a == b).all(1).sum())
-        total += a.shape[0]
-    return 100.0 * same / total
+def shape_launches(qs, qtype, imat, xs_rot, qws, outs):
+    tid = TYPE_IDS[qtype]
+    return [(lambda i, j=j: qs.quantize(tid, xs_rot[i % len(xs_rot)][j], qws[j] if imat else None,
+                                        out=outs[j]))
+            for j in range(len(SHAPES))]
+
+
+def gpu_bytes(torch, qs, qtype, imat, xs, qws):
+    """The GPU's bytes for the first input copy (both shapes), on the host."""
+    out = [qs.quantize(TYPE_IDS[qtype], x, qws[j] if imat else None) for j, x in enumerate(xs)]
+    torch.cuda.synchronize()
+    return [o.cpu().numpy() for o in out]
 
 
 def cpu_model() -> str:
@@ -177,27 +186,131 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(oracle, host, qws):
-    """The oracle on the full headline workload (Q4_K + imatrix), all host
-    cores; plus one thread on the first eighth of each tensor's rows."""
-    cores = len(os.sched_getaffinity(0))
+def compare_blocks(qtype, got, ref, x_f32, qw):
+    """Identical blocks of two packed outputs (one tensor), and for every
+    block that differs whether the GPU's imatrix-weighted MSE is <= the
+    oracle's (the tie rule): returns (blocks, identical, differing_with_le_mse)."""
+    import numpy as np
+    bb = BLOCK_BYTES[qtype]
+    a, b = got.reshape(-1, bb), ref.reshape(-1, bb)
+    same = (a == b).all(1)
+    le = 0
+    if not same.all():
+        if str(ROOT / "tests") not in sys.path:
+            sys.path.insert(0, str(ROOT / "tests"))
+        import dequant
+        rows = np.nonzero((~same).reshape(x_f32.shape[0], -1).any(1))[0]
+        ea = dequant.block_weighted_mse(qtype, got[rows], x_f32[rows], qw)
+        eb = dequant.block_weighted_mse(qtype, ref[rows], x_f32[rows], qw)
+        d = ~same.reshape(x_f32.shape[0], -1)[rows].reshape(-1)
+        le = int((ea[d] <= eb[d]).sum())
+    return int(same.size), int(same.sum()), le
 
-    def run(rows_frac, threads):
-        n = 0
+
+def cpu_baseline(oracle, host, qws, gpu_out: dict, seconds_per_type: float):
+    """The CPU leg: the oracle on this host's cores.
+      - value: the full headline workload (Q4_K + imatrix, both tensors), one
+        pass, all cores; plus one thread on the first eighth of each tensor;
+      - per_type: each type on the full tensors (or, past seconds_per_type of
+        projected CPU time, on the leading rows that fit), its CPU GB/s, and
+        its bytes compared with the GPU's: identical blocks and the tie rule."""
+    import numpy as np
+    cores = len(os.sched_getaffinity(0))
+    xf = [h.float().numpy() for h in host]
+    qwn = [q.cpu().numpy() for q in qws]
+
+    def run(qtype, imat, rows, threads):
+        outs, n = [], 0
         t0 = time.perf_counter()
         for j in range(len(SHAPES)):
-            x = host[j][: max(1, SHAPES[j][0] // rows_frac)].float().numpy()
-            oracle.quantize("q4_k", x, qws[j].cpu().numpy(), n_threads=threads)
+            x = xf[j][:rows[j]]
+            if x.shape[0] == 0:
+                continue
+            outs.append(oracle.quantize(qtype, x, qwn[j] if imat else None, n_threads=threads))
             n += x.size
-        return n, time.perf_counter() - t0
+        return outs, n, time.perf_counter() - t0
 
-    n, dt = run(1, cores)
-    n1, dt1 = run(8, 1)
+    full = [r for r, _ in SHAPES]
+    ref, n, dt = run("q4_k", True, full, cores)
+    _, n1, dt1 = run("q4_k", True, [r // 8 for r in full], 1)
+    per_type = {}
+    for key, outs in gpu_out.items():
+        qtype, imat = key.split("+")[0], key.endswith("+imat")
+        if key == "q4_k+imat":
+            refs, m, t = ref, n, dt
+        else:
+            # projected time from a 64-row probe of the first tensor
+            _, mp, tp = run(qtype, imat, [64, 0], cores)
+            frac = min(1.0, seconds_per_type / max(1e-9, tp / mp * n))
+            rows = [max(1, int(r * frac)) for r in full]
+            refs, m, t = run(qtype, imat, rows, cores)
+        blocks = same = le = 0
+        for j in range(len(SHAPES)):
+            r = refs[j].shape[0]
+            b, s, l = compare_blocks(qtype, outs[j][:r], refs[j], xf[j][:r], qwn[j] if imat else None)
+            blocks, same, le = blocks + b, same + s, le + l
+        print(f"bench: cpu leg {key}: {m} values in {t:.1f} s, {blocks - same} of {blocks} blocks "
+              f"differ", file=sys.stderr, flush=True)
+        per_type[key] = {"cpu_GBps": round(2 * m / t / 1e9, 4), "values_checked": int(m),
+                         "full_tensors": m == n,
+                         "identical_pct": round(100.0 * same / blocks, 4),
+                         "differing_blocks": blocks - same,
+                         "differing_with_le_weighted_mse": le}
     return {"value": round(2 * n / dt / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
             "value_1_thread": round(2 * n1 / dt1 / 1e9, 5), "cpu": cpu_model(),
             "sample": f"full workload: Q4_K+imatrix on bf16 {SHAPES[0][0]}x{SHAPES[0][1]} and "
                       f"{SHAPES[1][0]}x{SHAPES[1][1]} ({n} values), {dt:.2f} s, one pass; "
-                      f"1 thread: the first 1/8 of each tensor's rows ({n1} values), {dt1:.2f} s"}
+                      f"1 thread: the first 1/8 of each tensor's rows ({n1} values), {dt1:.2f} s",
+            "per_type": per_type}
+
+
+def config_c1(torch, qs, dev, steps: int) -> dict:
+    """Q4_0 on one 4096x4096 bf16 tensor, N(0, 0.02) with 0.1% of the values
+    (16,777, chosen with seed 0) scaled x20, no imatrix; 32 distinct copies
+    (1 GiB) rotate so the MALL cannot hold them."""
+    import numpy as np
+    rng = np.random.default_rng(0)
+    a = rng.normal(0.0, 0.02, (4096, 4096))
+    idx = rng.choice(a.size, 16777, replace=False)
+    a.reshape(-1)[idx] *= 20.0
+    x0 = bf16_from(torch, a).to(dev)
+    xs = [x0] + [x0.clone() for _ in range(31)]
+    out = torch.empty((4096, 4096 // 32 * 18), dtype=torch.uint8, device=dev)
+    wall, per = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 32], None, out=out)],
+                           max(steps, 64), 64)
+    alg = algorithmic_bytes("q4_0", 4096 * 4096, 4096) - 4 * 4096
+    return {"workload": "Q4_0 on bf16 4096x4096, N(0,0.02) + 0.1% outliers x20, seed 0",
+            "input_GBps": round(2 * 4096 * 4096 / (per[0] * 1e-3) / 1e9, 1),
+            "kernel_ms": round(per[0], 5), "ms_per_step": round(wall, 5),
+            "hbm_frac": round(alg / (per[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def config_c4(torch, qs, dev, steps: int) -> dict:
+    """IQ2_XXS + imatrix on 36 ffn_down tensors of 2560x9728 bf16: Student-t
+    (df 5) weights scaled to std 0.02, a log-normal imatrix per tensor. One
+    step = the 36 tensors."""
+    g = torch.Generator(device=dev).manual_seed(4)
+    rows, k, n = 2560, 9728, 36
+    scale = 0.02 / (5.0 / 3.0) ** 0.5
+    xs, qws = [], []
+    for _ in range(n):
+        # Student-t(5) = N(0,1) / sqrt(chi2(5) / 5)
+        z = torch.randn(rows, k, device=dev, generator=g)
+        c = torch.randn(5, rows, k, device=dev, generator=g).pow_(2).sum(0).div_(5.0).sqrt_()
+        xs.append((z / c * scale).to(torch.bfloat16))
+        qws.append(torch.randn(k, device=dev, generator=g).exp_())
+        del z, c
+    out = torch.empty((rows, k // 256 * 66), dtype=torch.uint8, device=dev)
+    launches = [(lambda i, j=j: qs.quantize(16, xs[j], qws[j], out=out)) for j in range(n)]
+    wall, per = time_steps(torch, launches, max(1, steps // 50), 1)
+    kms = sum(per) / n
+    return {"workload": "IQ2_XXS + imatrix on 36 ffn_down tensors 2560x9728 bf16, Student-t df 5 "
+                        "scaled to std 0.02, log-normal imatrix",
+            "input_GBps": round(2 * rows * k * n / (wall * 1e-3) / 1e9, 2),
+            "ms_per_step": round(wall, 3), "kernel_ms_mean": round(kms, 4),
+            "kernel_GBps": round(2 * rows * k / (kms * 1e-3) / 1e9, 2),
+            "hbm_frac": round(algorithmic_bytes("iq2_xxs", rows * k, k) / (kms * 1e-3) / 1e9
+                              / HBM_PEAK_GBS, 5)}
 
 
 def q4_0_large(torch, qs, dev, steps: int) -> dict:
@@ -207,24 +320,12 @@ def q4_0_large(torch, qs, dev, steps: int) -> dict:
     g = torch.Generator(device=dev).manual_seed(1)
     xs = [(torch.randn(rows, k, device=dev, generator=g) * 0.01).to(torch.bfloat16) for _ in range(2)]
     out = torch.empty((rows, k // 32 * 18), dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream()
-    # ~6 ms of warm-up: the first launches after the other kernels run below
-    # the GPU's sustained clocks; then the median of three timed groups
-    for i in range(30):
-        qs.quantize(2, xs[i % 2], None, out=out)
-    groups = []
-    for _ in range(3):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for i in range(steps):
-            qs.quantize(2, xs[i % 2], None, out=out)
-        b.record(stream)
-        torch.cuda.synchronize()
-        groups.append(a.elapsed_time(b) / steps)
-    ms = sorted(groups)[1]
+    wall, per = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 2], None, out=out)], steps, 30)
+    ms = per[0]
     alg = algorithmic_bytes("q4_0", rows * k, k) - 4 * k
     return {"input_GBps": round(2 * rows * k / (ms * 1e-3) / 1e9, 1), "kernel_ms": round(ms, 4),
-            "hbm_GBps": round(alg / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "hbm_GBps": round(alg / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def copy_peak(torch, dev, steps: int, warmup: int) -> int:
@@ -232,17 +333,11 @@ def copy_peak(torch, dev, steps: int, warmup: int) -> int:
     nbytes = 1 << 30
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
-    for _ in range(warmup):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        b.copy_(a)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / steps
+    wall, per = time_steps(torch, [lambda i: b.copy_(a)], steps, warmup)
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
-                      "ms_per_copy": round(dt * 1e3, 4),
-                      "copy_GBps_read_plus_write": round(2 * nbytes / dt / 1e9, 1)}), flush=True)
+                      "ms_per_copy": round(per[0], 4),
+                      "copy_GBps_read_plus_write": round(2 * nbytes / (per[0] * 1e-3) / 1e9, 1)}),
+          flush=True)
     return 0
 
 
@@ -305,53 +400,101 @@ def synth_model(torch, dev, path: Path, im_path: Path, seed: int = 0) -> int:
     return n_weights
 
 
-def run_e2e(torch, dev, schemes: list[str]) -> int:
+def fs_type(path: Path) -> str:
+    """Filesystem type of the mount holding `path` (/proc/mounts)."""
+    best, kind = "", "unknown"
+    p = str(path.resolve())
+    try:
+        for ln in open("/proc/mounts"):
+            parts = ln.split()
+            if len(parts) > 2 and (p == parts[1] or p.startswith(parts[1].rstrip("/") + "/")) \
+                    and len(parts[1]) >= len(best):
+                best, kind = parts[1], parts[2]
+    except OSError:
+        pass
+    return kind
+
+
+def drop_page_cache(path: Path) -> None:
+    """Evict a file's clean pages (fsync, then POSIX_FADV_DONTNEED)."""
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.fsync(fd)
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+    finally:
+        os.close(fd)
+
+
+def run_e2e(torch, dev, schemes: list[str], where: str | None) -> int:
+    """The command line on the synthetic model, per scheme: one run with the
+    input in the page cache (warm) and one after evicting the input and the
+    imatrix from it (cold; only meaningful on a disk-backed filesystem)."""
     import re
     import subprocess
     import tempfile
-    base = Path("/dev/shm") if Path("/dev/shm").is_dir() else Path(tempfile.gettempdir())
-    with tempfile.TemporaryDirectory(dir=base) as d:
+    cands = [Path(where)] if where else [Path(os.environ.get("TMPDIR", "/tmp")), Path("/tmp"),
+                                         Path("/var/tmp"), ROOT]
+    base = next((c for c in cands if c.is_dir() and fs_type(c) not in ("tmpfs", "ramfs")), cands[0])
+    with tempfile.TemporaryDirectory(dir=base, prefix="qs_e2e_") as d:
         d = Path(d)
         src, im = d / "model-bf16.gguf", d / "imatrix.gguf"
         t0 = time.perf_counter()
         n = synth_model(torch, dev, src, im)
         gen_s = time.perf_counter() - t0
+        print(f"e2e: model written to {d} ({fs_type(d)}) in {gen_s:.1f} s", file=sys.stderr, flush=True)
         results = {}
         for sch in schemes:
             name, *extra = sch.split()
-            out = d / f"out-{name}.gguf"
-            cmd = [sys.executable, str(ROOT / "quant-studio.py"), str(src), str(out), name,
-                   "--imatrix", str(im), *extra]
-            t0 = time.perf_counter()
-            r = subprocess.run(cmd, capture_output=True, text=True)
-            wall = time.perf_counter() - t0
-            if r.returncode != 0:
-                print(r.stderr[-2000:], file=sys.stderr)
-                return 1
-            m = re.search(r"done in ([0-9.]+)s", r.stdout)
-            results[sch] = {"pipeline_s": float(m.group(1)) if m else None,
-                            "process_wall_s": round(wall, 2),
-                            "input_GBps_pipeline": round(src.stat().st_size / 1e9 / float(m.group(1)), 2)
-                            if m and float(m.group(1)) > 0 else None,
-                            "out_bytes": out.stat().st_size}
-            out.unlink()
-            print(f"e2e {sch}: {results[sch]}", file=sys.stderr, flush=True)
-        print(json.dumps({"e2e": "synthetic 4B-class bf16 GGUF (36 layers, 2560/9728, vocab 151936), "
-                                 "file in page cache", "file_bytes": src.stat().st_size,
-                          "weights": n, "generate_s": round(gen_s, 1), "runs": results}), flush=True)
+            for cache in ("warm", "cold"):
+                out = d / f"out-{name}.gguf"
+                if cache == "cold":
+                    drop_page_cache(src)
+                    drop_page_cache(im)
+                cmd = [sys.executable, str(ROOT / "quant-studio.py"), str(src), str(out), name,
+                       "--imatrix", str(im), *extra]
+                t0 = time.perf_counter()
+                r = subprocess.run(cmd, capture_output=True, text=True)
+                wall = time.perf_counter() - t0
+                if r.returncode != 0:
+                    print(r.stderr[-2000:], file=sys.stderr)
+                    return 1
+                m = re.search(r"done in ([0-9.]+)s", r.stdout)
+                pipe_s = float(m.group(1)) if m else None
+                results[f"{sch} {cache}"] = {
+                    "pipeline_s": pipe_s, "process_wall_s": round(wall, 2),
+                    "input_GBps_pipeline": round(src.stat().st_size / 1e9 / pipe_s, 2)
+                    if pipe_s else None,
+                    "out_bytes": out.stat().st_size}
+                out.unlink()
+                print(f"e2e {sch} {cache}: {results[f'{sch} {cache}']}", file=sys.stderr, flush=True)
+        print(json.dumps({"e2e": "synthetic 4B-class bf16 GGUF (36 layers, 2560/9728, vocab 151936)",
+                          "filesystem": fs_type(d), "file_bytes": src.stat().st_size,
+                          "weights": n, "generate_s": round(gen_s, 1),
+                          "cold": "input and imatrix evicted from the page cache before the run "
+                                  "(fsync + POSIX_FADV_DONTNEED)",
+                          "runs": results}), flush=True)
     return 0
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--types", default="all", help="per-type table: all, none or a comma list")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the Q4_0 4096x4096 and "
+                    "IQ2_XXS Student-t workloads")
+    ap.add_argument("--cpu-seconds", type=float, default=45.0,
+                    help="CPU time per type for the identical-block check (full tensors when "
+                         "the oracle fits in it)")
+    ap.add_argument("--sqrt", default="torch-cpu", choices=["torch-cpu", "ieee", "torch-cpu-amd"],
+                    help="square-root rounding of the weights (the oracle follows it)")
     ap.add_argument("--e2e", default=None,
                     help="run the CLI end to end on a synthetic 4B-class model for these "
                          "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M') and print its own JSON line")
+    ap.add_argument("--e2e-dir", default=None, help="directory for the e2e model (default: the "
+                    "first disk-backed of $TMPDIR, /tmp, /var/tmp, the repository)")
     ap.add_argument("--valu-peak", action="store_true",
                     help="time the VALU issue-rate kernel only (the reference for SQ_INSTS_VALU)")
     ap.add_argument("--copy-only", action="store_true",
@@ -359,13 +502,13 @@ def main() -> int:
                          "reference size for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE counts)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this quantizer runs on one GPU; --gpus must be 1 "
-              "(the path shards by tensor with no exchange, see the design notes)", file=sys.stderr)
+        print("bench.py: this quantizer runs on one GPU; --gpus must be 1 (the path shards by "
+              "tensor with no exchange between GPUs, so a single GPU's rate is what it measures)",
+              file=sys.stderr)
         return 2
 
     import torch
     qs = importlib.import_module("quant-studio_amd")
-    import oracle
 
     dev = torch.device("cuda:0")
     if args.copy_only:
@@ -374,7 +517,9 @@ def main() -> int:
         print(json.dumps({"valu_wave_instr_per_s": round(valu_peak(torch, dev, args.steps))}), flush=True)
         return 0
     if args.e2e:
-        return run_e2e(torch, dev, [x.strip() for x in args.e2e.split(";") if x.strip()])
+        return run_e2e(torch, dev, [x.strip() for x in args.e2e.split(";") if x.strip()], args.e2e_dir)
+    qs.set_sqrt_rounding(args.sqrt)
+    qs.init(0)
     xs, qws, host = make_inputs(torch, dev)
     per_step_bytes = sum(2 * r * k for r, k in SHAPES)
     nrot = max(1, -(-ROTATE_BYTES // per_step_bytes))
@@ -385,28 +530,31 @@ def main() -> int:
         return [torch.empty((r, k // 256 * OUT_BYTES_PER_256[qtype]), dtype=torch.uint8, device=dev)
                 for r, k in SHAPES]
 
-    # headline: Q4_K + imatrix
-    ms_step, kms = time_type(torch, qs, "q4_k", True, xs_rot, qws, outs_for("q4_k"),
-                             args.steps, args.warmup)
+    # headline: Q4_K + imatrix; the dominant kernel is the 9728x2560 launch
+    ms_step, kms = time_steps(torch, shape_launches(qs, "q4_k", True, xs_rot, qws, outs_for("q4_k")),
+                              args.steps, args.warmup)
     value = 2 * n_elems / (ms_step * 1e-3) / 1e9
-    # dominant kernel: the 9728x2560 launch
+    print(f"bench: headline {ms_step:.4f} ms per step, {kms[0]:.4f} / {kms[1]:.4f} ms per launch",
+          file=sys.stderr, flush=True)
     r0, k0 = SHAPES[0]
     alg = algorithmic_bytes("q4_k", r0 * k0, k0)
     achieved = alg / (kms[0] * 1e-3) / 1e9
-
-    per_type = {}
-    valu_counts = profiled_valu_per_type()
+    insts = profile_figure("counters_q4_k_imat_9728x2560.md", "valu_insts_per_launch")
+    traffic = profile_figure("counters_q4_k_imat_9728x2560.md", "traffic_bytes_per_launch")
     peak_valu = valu_peak(torch, dev)
+
+    per_type, gpu_out = {}, {}
+    valu_counts = profiled_valu_per_type()
     sel = [] if args.types == "none" else (list(TYPE_IDS) if args.types == "all"
                                            else args.types.split(","))
     for qtype in sel:
-        modes = (False,) if qtype in IGNORE_IMATRIX else (True,) if qtype in NEEDS_IMATRIX else (False, True)
-        for imat in modes:
-            st, km = time_type(torch, qs, qtype, imat, xs_rot, qws, outs_for(qtype),
-                               max(3, args.steps // 4), 1)
-            a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
+        for imat in modes_of(qtype):
             key = f"{qtype}{'+imat' if imat else ''}"
-            insts = valu_counts.get(key)
+            st, km = time_steps(torch, shape_launches(qs, qtype, imat, xs_rot, qws, outs_for(qtype)),
+                                max(10, args.steps // 4), 5)
+            a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
+            n_insts = valu_counts.get(key)
+            print(f"bench: {key}: {km[0]:.4f} / {km[1]:.4f} ms per launch", file=sys.stderr, flush=True)
             per_type[key] = {
                 "input_GBps": round(2 * n_elems / (st * 1e-3) / 1e9, 2),
                 "ms_per_step": round(st, 4),
@@ -414,15 +562,22 @@ def main() -> int:
                 "hbm_frac": round(a / HBM_PEAK_GBS, 4),
                 # VALU issue rate (SQ_INSTS_VALU per launch over the live launch
                 # time) against the calibration kernel's rate
-                "valu_frac": None if insts is None else
-                round(insts / (sum(km) / len(km) * 1e-3) / peak_valu, 3),
-                "identical_pct_vs_oracle": round(identical_pct(torch, qs, oracle, qtype, imat,
-                                                               host, qws), 3),
+                "valu_frac": None if n_insts is None else
+                round(n_insts / (sum(km) / len(km) * 1e-3) / peak_valu, 3),
             }
+            if not args.no_cpu:
+                gpu_out[key] = gpu_bytes(torch, qs, qtype, imat, xs, qws)
+    if not args.no_cpu and "q4_k+imat" not in gpu_out:
+        gpu_out["q4_k+imat"] = gpu_bytes(torch, qs, "q4_k", True, xs, qws)
 
+    configs = {}
+    if not args.no_configs:
+        del xs_rot
+        configs["c1_q4_0_4096x4096"] = config_c1(torch, qs, dev, args.steps)
+        configs["c4_iq2_xxs_imat_36x2560x9728_student_t"] = config_c4(torch, qs, dev, args.steps)
+        torch.cuda.empty_cache()
     if "q4_0" in sel:
         per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
-    insts = profiled("valu_insts_per_launch")
 
     line = {
         "metric": "input GB/s (bf16) per quant type at 1 GPU + % identical blocks vs reference",
@@ -439,24 +594,37 @@ def main() -> int:
         "data": "synthetic (seeded bf16 tensors resident in HBM, rotated over >=1 GiB)",
         "config": {"workload": "Q4_K + imatrix on bf16 ffn tensors 9728x2560 and 2560x9728",
                    "types": "q4_k", "imatrix": True, "n_values": n_elems,
-                   "parallelism": "1 GPU (no exchange)"},
+                   "sqrt_rounding": args.sqrt, "parallelism": "1 GPU (no exchange)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
-                     "traffic": profiled("traffic_bytes_per_launch"),
+                     "traffic": None if traffic is None else int(traffic),
                      "kernel": "k_q45_k<bf16, imatrix, 15>", "kernel_ms": round(kms[0], 4),
+                     "kernel_ms_per_shape": [round(v, 4) for v in kms],
                      "algorithmic_bytes": alg,
-                     # the kernel is VALU-bound: its SQ_INSTS_VALU per launch over its
-                     # live duration, against the measured issue rate of a pure
-                     # mul/add kernel
+                     # the binding roof: this kernel is VALU-bound, so its
+                     # SQ_INSTS_VALU per launch over the same live duration is
+                     # set against the measured issue rate of a pure mul/add kernel
+                     "binding": "valu",
                      "valu": None if insts is None else {
-                         "insts_per_launch": insts, "unit": "G wave-instr/s",
+                         "insts_per_launch": int(insts), "unit": "G wave-instr/s",
                          "achieved": round(insts / (kms[0] * 1e-3) / 1e9, 1),
                          "peak": round(peak_valu / 1e9, 1),
                          "frac": round(insts / (kms[0] * 1e-3) / peak_valu, 4)}},
         "per_type": per_type,
+        "configs": configs,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(oracle, host, qws)
+        import oracle
+        if args.sqrt == "ieee":
+            oracle.use_ieee_sqrt(True)
+        elif args.sqrt == "torch-cpu-amd":
+            sys.path.insert(0, str(ROOT / "tests"))
+            import sqrt_hosts
+            oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+        cb = cpu_baseline(oracle, host, qws, gpu_out, args.cpu_seconds)
+        line["cpu_baseline"] = cb
+        head = cb["per_type"].get("q4_k+imat")
+        line["identical_pct_vs_oracle"] = None if head is None else head["identical_pct"]
     print(json.dumps(line), flush=True)
     return 0
 

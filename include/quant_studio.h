@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QS_ABI_VERSION 2
+#define QS_ABI_VERSION 3
 
 #define QS_EINVAL (-22)
 #define QS_ENOTSUP (-95)
@@ -64,6 +64,38 @@ extern "C" {
 /* Version of this ABI (QS_ABI_VERSION). */
 int qs_abi_version(void);
 
+/* Upload the constant tables the quantizers read (the square-root map and
+ * every IQ grid / neighbour-list table, about 7.5 MB) to `device` now, with
+ * blocking copies, and keep them until the process ends. qs_quantize() does
+ * the same lazily on its first call per device (and per IQ grid): a
+ * hipMalloc plus a blocking hipMemcpy inside that call. Callers that must not
+ * allocate or synchronise inside qs_quantize (stream capture into a graph, a
+ * latency-critical loop) call qs_init() for each device first; every later
+ * qs_quantize() on that device then only launches. The reference builds its
+ * tables lazily per kernel module (tables_for, kernels/iq2.py:80-84,
+ * iq2xs_common.py:101-106, iq3_common.py:81-85). */
+int qs_init(int device);
+
+/* Square-root rounding of the weights sqrt(sigma2 + x^2) and sqrt(w) that the
+ * K-quant, IQ4 and IQ quantizers with an imatrix (and Q4_K/Q5_K without one)
+ * compute. The reference takes them with torch.sqrt (e.g. kernels/q4_k.py:34,
+ * :51; iq2.py:431-436), whose rounding depends on where it runs:
+ *   QS_SQRT_TORCH_CPU      torch.sqrt on a CPU tensor on an Intel x86-64 host
+ *                          (MKL: one ulp below the IEEE root on 98,955 of the
+ *                          2^24 mantissa/parity classes), the host that wrote
+ *                          the golden vectors; the default
+ *   QS_SQRT_IEEE           the correctly rounded root (torch.sqrt on a GPU
+ *                          tensor, as on the reference's CUDA path; C sqrtf)
+ *   QS_SQRT_TORCH_CPU_AMD  torch.sqrt on a CPU tensor on an AMD EPYC host (the
+ *                          MI355X box's; MKL there: one ulp below on 7.4% and
+ *                          one ulp above on 9.8% of the classes)
+ * Process-wide; read by each qs_quantize() call at launch. */
+#define QS_SQRT_TORCH_CPU 0
+#define QS_SQRT_IEEE 1
+#define QS_SQRT_TORCH_CPU_AMD 2
+int qs_set_sqrt_rounding(int mode);
+int qs_get_sqrt_rounding(void);
+
 /* 1 if ggml_type has a HIP quantizer in this build, else 0. Mirrors the
  * registry membership test `type in QUANT_TYPES` (kernels/__init__.py:18-27,
  * quant-studio.py:396-399). */
@@ -92,8 +124,14 @@ int64_t qs_row_bytes(int ggml_type, int64_t k);
  *   hip_stream:    hipStream_t to launch on (NULL = null stream)
  * At most 2^34 values (n_rows * k) per call, and n_rows * src_row_stride_bytes
  * below 2^62; larger calls are refused with QS_EINVAL (split them by rows).
- * Asynchronous and stream-ordered; allocates nothing. The output bytes do not
- * depend on how rows are split across calls. */
+ * Asynchronous and stream-ordered: the kernel is queued on hip_stream and the
+ * call returns; the launch status is the return value (the caller's
+ * hipGetLastError() state is left alone). The kernels use no device memory
+ * beyond src, imatrix, dst and the constant tables; the first call per device
+ * (and per IQ grid) uploads those tables (hipMalloc and a blocking copy,
+ * under a process-wide lock) unless qs_init() did. Every call takes that lock
+ * briefly to look the tables up. Safe to call from several threads. The output
+ * bytes do not depend on how rows are split across calls. */
 int qs_quantize(int ggml_type, int src_type, const void *src, int64_t n_rows, int64_t k,
                 int64_t src_row_stride_bytes, const float *imatrix, void *dst,
                 int64_t dst_bytes, void *hip_stream);

@@ -58,6 +58,10 @@ def lib() -> ctypes.CDLL:
         L.qso_set_sqrt_hook.argtypes = [ctypes.c_void_p]
         L.qso_set_sqrt_ieee.restype = None
         L.qso_set_sqrt_ieee.argtypes = [ctypes.c_int]
+        L.qso_set_sqrt_table.restype = None
+        L.qso_set_sqrt_table.argtypes = [ctypes.c_void_p]
+        L.qso_sqrt.restype = ctypes.c_float
+        L.qso_sqrt.argtypes = [ctypes.c_float]
         L.qso_sqrt_ref.restype = ctypes.c_float
         L.qso_sqrt_ref.argtypes = [ctypes.c_float]
         L.qso_set_mutation.restype = None
@@ -108,6 +112,25 @@ def sqrt_ref(v: float) -> np.float32:
 def use_ieee_sqrt(enable: bool) -> None:
     """Make the oracle use plain IEEE sqrtf for its weights (tests only)."""
     lib().qso_set_sqrt_ieee(1 if enable else 0)
+
+
+_sqrt_table = None
+
+
+def use_sqrt_table(ulps) -> None:
+    """Make the oracle round its square roots by a per-key table: `ulps` holds
+    2^24 int8 offsets from the IEEE root (torch.sqrt measured on another host),
+    keyed like qso_sqrt_ref; None switches the table off (tests only)."""
+    global _sqrt_table
+    if ulps is None:
+        lib().qso_set_sqrt_table(None)
+        _sqrt_table = None
+        return
+    t = np.ascontiguousarray(ulps, dtype=np.int8)
+    if t.size != 1 << 24:
+        raise ValueError("the square-root table holds one offset per 2^24 keys")
+    lib().qso_set_sqrt_table(t.ctypes.data)
+    _sqrt_table = t
 
 
 def use_torch_sqrt(enable: bool) -> None:

@@ -30,7 +30,10 @@
 static int g_mut = 0;
 void qso_set_mutation(int m) { g_mut = m; }
 enum { MUT_IEEE_RDIV = 1, MUT_SEQ_CASCADE = 2, MUT_SEQ_TREE = 3, MUT_DROP_STEP = 4,
-       MUT_ROUND_AWAY = 5, MUT_ACCEPT_GE = 6 };
+       MUT_ROUND_AWAY = 5, MUT_ACCEPT_GE = 6,
+       /* the 32-value formats without a reference module: d = a * (1/n) instead of
+        * the IEEE a / n, and x / d instead of x * (1/d) */
+       MUT_D_BY_RECIP = 7, MUT_X_DIV_D = 8 };
 
 /* torch: python_float / tensor  ->  tensor.reciprocal() * python_float */
 static inline float RDIV(float c, float t) {
@@ -82,14 +85,38 @@ float qso_sqrt_ref(float v) {
     return r;
 }
 
+/* Another host's torch.sqrt rounding, given as a per-key offset in ulps from
+ * the IEEE root (2^24 int8 entries, same keys as above): the rounding measured
+ * on a host whose MKL takes a different code path (tests only). */
+static const int8_t *g_sqrt_ulps = 0;
+void qso_set_sqrt_table(const int8_t *ulps) { g_sqrt_ulps = ulps; }
+static float sqrt_table_ulps(float v) {
+    float r = sqrtf(v);
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    if (b - 1u < 0x7f7fffffu) {
+        if (b < 0x00800000u) {
+            float n = v * 18446744073709551616.0f;
+            memcpy(&b, &n, 4);
+        }
+        uint32_t key = ((((b >> 23) & 1u) ^ 1u) << 23) | (b & 0x7fffffu), rb;
+        memcpy(&rb, &r, 4);
+        rb = (uint32_t)((int32_t)rb + g_sqrt_ulps[key]);
+        memcpy(&r, &rb, 4);
+    }
+    return r;
+}
+
 static float (*g_sqrt_hook)(float) = 0;
 static int g_sqrt_ieee = 0;
 void qso_set_sqrt_hook(float (*fn)(float)) { g_sqrt_hook = fn; }
 void qso_set_sqrt_ieee(int on) { g_sqrt_ieee = on; }
 static inline float SQRT(float v) {
     if (g_sqrt_hook) return g_sqrt_hook(v);
+    if (g_sqrt_ulps) return sqrt_table_ulps(v);
     return g_sqrt_ieee ? sqrtf(v) : qso_sqrt_ref(v);
 }
+float qso_sqrt(float v) { return SQRT(v); }
 static inline float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi); }
 
 /* ------------------------------------------------------------------ */
@@ -809,27 +836,38 @@ static void iq4_xs_block(const float *x, const float *qw, uint8_t *out) {
 /* dequantisation bounds and special blocks (tests/test_oracle.py), and   */
 /* IQ4_NL's search by the IQ4_XS golden vectors it shares.               */
 /* ------------------------------------------------------------------ */
+/* planted-slip helpers (tests only): a / n and x * id as written, or slipped */
+static inline float DIV_N(float a, float n) { return g_mut == MUT_D_BY_RECIP ? a * (1.0f / n) : a / n; }
+static inline float MUL_ID(float x, float id, float d) { return g_mut == MUT_X_DIV_D && d != 0 ? x / d : x * id; }
+
 static void q8_0_block(const float *b, uint8_t *out) {
     float am = 0.0f;
     for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(b[i]));
-    float d = am / 127.0f;
+    float d = DIV_N(am, 127.0f);
     float id = d != 0 ? 1.0f / d : 0.0f;
     put_f16(out, d);
-    for (int i = 0; i < 32; i++) out[2 + i] = (uint8_t)(int8_t)(int)roundf(b[i] * id);  /* half away from 0 */
+    /* half away from zero (C roundf). A d below 127 * 2^-128 makes 1/d infinite
+     * and x * id infinite or NaN, where C's conversion is undefined: such values
+     * saturate to [-128, 127] and NaN gives 0 (the kernels do the same). */
+    for (int i = 0; i < 32; i++) {
+        float r = roundf(MUL_ID(b[i], id, d));
+        out[2 + i] = (uint8_t)(int8_t)(r != r ? 0 : (int)clampf(r, -128.0f, 127.0f));
+    }
 }
 
 /* Q4_1 (nmax 15) and Q5_1 (nmax 31): d = (max - min) / nmax, m = min */
 static void q_1_block(const float *b, uint8_t *out, int nmax) {
     float mn = b[0], mx = b[0];
     for (int i = 1; i < 32; i++) { mn = fminf(mn, b[i]); mx = fmaxf(mx, b[i]); }
-    float d = (mx - mn) / (float)nmax;
+    float d = DIV_N(mx - mn, (float)nmax);
     float id = d != 0 ? 1.0f / d : 0.0f;
     uint8_t q[32];
     for (int i = 0; i < 32; i++) {
         float t = b[i] - mn;
-        t = t * id;
+        t = MUL_ID(t, id, d);
         t = t + 0.5f;
-        q[i] = (uint8_t)fminf(truncf(t), (float)nmax);
+        /* clamp to [0, nmax] (t >= 0.5 unless 1/d overflowed; NaN gives 0) */
+        q[i] = (uint8_t)clampf(truncf(t), 0.0f, (float)nmax);
     }
     put_f16(out, d);
     put_f16(out + 2, mn);
@@ -852,7 +890,7 @@ static void q5_0_block(const float *b, uint8_t *out) {
     float id = d != 0 ? 1.0f / d : 0.0f;
     uint8_t q[32];
     for (int i = 0; i < 32; i++) {
-        float t = b[i] * id;
+        float t = MUL_ID(b[i], id, d);
         t = t + 16.5f;
         q[i] = (uint8_t)clampf(floorf(t), 0.0f, 31.0f);
     }
@@ -878,7 +916,8 @@ static void iq4_nl_block(const float *x, const float *qw, uint8_t *out) {
     float id = d != 0 ? 1.0f / d : 0.0f;
     put_f16(out, d);
     for (int j = 0; j < 16; j++)
-        out[2 + j] = (uint8_t)(iq4_best_index(id * x[j]) | (iq4_best_index(id * x[j + 16]) << 4));
+        out[2 + j] = (uint8_t)(iq4_best_index(MUL_ID(x[j], id, d)) |
+                               (iq4_best_index(MUL_ID(x[j + 16], id, d)) << 4));
 }
 
 /* ------------------------------------------------------------------ */

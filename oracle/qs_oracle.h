@@ -49,6 +49,12 @@ void qso_set_mutation(int m);
 float qso_sqrt_ref(float v);
 void qso_set_sqrt_hook(float (*fn)(float));
 void qso_set_sqrt_ieee(int on);
+/* Test hook: a per-key rounding table (2^24 int8 ulp offsets from the IEEE
+ * root, keyed as qso_sqrt_ref; NULL = off), e.g. torch.sqrt measured on
+ * another host. The caller keeps the table alive while it is installed. */
+void qso_set_sqrt_table(const int8_t *ulps);
+/* The square root the weights currently use (whichever of the above is set). */
+float qso_sqrt(float v);
 /* Neighbour list of an off-grid code (tables 0..4: IQ2 256/512/1024, IQ3 256/512):
  * writes up to cap grid indices, returns the list length (0 for on-grid codes). */
 int qso_neighbours(int which, int code, uint16_t *out, int cap);

@@ -4,10 +4,13 @@ Mirrors the reference's kernel registry (kernels/__init__.py:18-27,
 kernels/common.py:20-37): `QUANT_TYPES` maps a lowercase type name to a
 `QuantSpec`, whose `make_kernel(device, qw)` returns `quant_fn(x) -> uint8`.
 Here every quant_fn is one call into the gfx950 HIP library (libqs_hip.so,
-C ABI in include/quant_studio.h) on torch's current stream. There is no CPU
-path: the library must be built (build.py) and a ROCm device present, and
-every failure raises. torch is imported on first use of the tensor API only;
-the command line runs on the library's own pipeline without it.
+C ABI in include/quant_studio.h) on torch's current stream. A quant_fn made
+for a CPU device (the reference's CPU path, quant-studio.py:216-232) takes
+CPU tensors and returns a CPU tensor, computing on the current ROCm device
+(the bytes are the reference CPU path's either way). There is no CPU
+arithmetic: the library must be built (build.py) and a ROCm device present,
+and every failure raises. torch is imported on first use of the tensor API
+only; the command line runs on the library's own pipeline without it.
 
 Import with `importlib.import_module("quant-studio_amd")` (the directory name
 is not an identifier).
@@ -23,7 +26,7 @@ from .gguf_types import GGMLQuantizationType, LlamaFileType
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "_build" / "libqs_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib: ctypes.CDLL | None = None
 
@@ -91,6 +94,11 @@ def library() -> ctypes.CDLL:
         L.qs_quantize.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                   ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                   ctypes.c_int64, ctypes.c_void_p]
+        L.qs_init.restype = ctypes.c_int
+        L.qs_init.argtypes = [ctypes.c_int]
+        L.qs_set_sqrt_rounding.restype = ctypes.c_int
+        L.qs_set_sqrt_rounding.argtypes = [ctypes.c_int]
+        L.qs_get_sqrt_rounding.restype = ctypes.c_int
         L.qs_last_error.restype = ctypes.c_char_p
         L.qs_device_count.restype = ctypes.c_int
         L.qs_pipeline_create.restype = ctypes.c_int
@@ -126,23 +134,78 @@ def row_bytes(ggml_type: int, k: int) -> int:
 
 MAX_VALUES_PER_CALL = 1 << 34      # qs_quantize's per-call limit (include/quant_studio.h)
 
+# square-root rounding of the weights (QS_SQRT_* in include/quant_studio.h):
+# torch.sqrt on an Intel host's CPU (the default), the IEEE root, torch.sqrt on
+# an AMD EPYC host's CPU
+SQRT_ROUNDING = {"torch-cpu": 0, "ieee": 1, "torch-cpu-amd": 2}
+
+
+def init(device: int = 0) -> None:
+    """Upload the library's constant tables to ROCm device `device` now
+    (qs_init), so no later quant_fn call on it allocates or blocks."""
+    if library().qs_init(int(device)) != 0:
+        raise QuantSpecError(last_error())
+
+
+def set_sqrt_rounding(mode: str) -> None:
+    """Square-root rounding of the weights, process-wide: "torch-cpu" (the
+    default: torch.sqrt on an Intel host's CPU, where the golden vectors were
+    written), "ieee" (the correctly rounded root: torch.sqrt on a GPU tensor,
+    C sqrtf) or "torch-cpu-amd" (torch.sqrt on an AMD EPYC host's CPU)."""
+    if mode not in SQRT_ROUNDING:
+        raise ValueError(f"square-root rounding {mode!r}: one of {', '.join(SQRT_ROUNDING)}")
+    if library().qs_set_sqrt_rounding(SQRT_ROUNDING[mode]) != 0:
+        raise QuantSpecError(last_error())
+
+
+def sqrt_rounding() -> str:
+    code = library().qs_get_sqrt_rounding()
+    return next(name for name, c in SQRT_ROUNDING.items() if c == code)
+
+
+def _rocm_device():
+    import torch
+    if not torch.cuda.is_available():
+        raise QuantSpecError("quant_fn: no ROCm device; this build computes every type on the GPU "
+                             "(a CPU tensor is staged through the current ROCm device)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _quantize_host(ggml_type: int, x, qw, out):
+    """A CPU (or other non-ROCm) x: copy it and qw to the current ROCm device,
+    quantize there and return the bytes on x's device (synchronous)."""
+    dev = _rocm_device()
+    q = None if qw is None else qw.to(dev)
+    got = quantize(ggml_type, x.to(dev), q)
+    if out is None:
+        return got.to(x.device)
+    out.view(got.shape).copy_(got)
+    return out
+
 
 def quantize(ggml_type: int, x, qw, out=None):
-    """Quantize the rows of x (n, k) on its ROCm device; returns uint8 (n, row_bytes).
+    """Quantize the rows of x (n, k); returns uint8 (n, row_bytes) on x's device.
 
-    x: float32 / float16 / bfloat16, unit stride along k, 16-byte aligned rows.
-    qw: (k,) float32 imatrix column weights on the same device, or None.
-    The launch goes on torch's current stream; nothing is synchronised."""
+    x: float32 / float16 / bfloat16, any strides (layouts the C call does not
+    take -- a column stride other than 1, rows not 16-byte aligned, a row
+    stride that is not a multiple of 16 bytes or shorter than a row -- are
+    copied to a contiguous tensor first).
+    qw: (k,) float32 imatrix column weights on x's device, or None.
+    On a ROCm device the launch goes on torch's current stream and nothing is
+    synchronised; a tensor on any other device is staged through the current
+    ROCm device and the call returns when the bytes are back."""
     import torch
-    if x.device.type != "cuda":
-        raise ValueError(f"quant_fn: x must be on a ROCm device, got {x.device}")
     if x.dim() != 2:
         raise ValueError(f"quant_fn: x must be 2-D (n, k), got shape {tuple(x.shape)}")
     src_id = _src_id(x.dtype)
     if src_id is None:
         raise ValueError(f"quant_fn: unsupported dtype {x.dtype}")
+    if x.device.type != "cuda":
+        return _quantize_host(ggml_type, x, qw, out)
     n, k = x.shape
-    if x.stride(1) != 1 and k > 1:
+    esz = x.element_size()
+    if n > 0 and ((k > 1 and x.stride(1) != 1) or x.data_ptr() % 16 or
+                  (n > 1 and (x.stride(0) < k or (x.stride(0) * esz) % 16))):
         x = x.contiguous()
     rb = row_bytes(ggml_type, k)
     if out is None:
@@ -191,7 +254,20 @@ def _kernel_factory(ggml_type: GGMLQuantizationType, uses_imatrix: bool):
                                             # the other 32-value integer formats
         if q is not None:
             q = q.to(device=device, dtype=torch.float32).contiguous()
-        return lambda x: quantize(ggml_type, x, q)
+        if torch.device(device).type == "cuda" or q is None:
+            return lambda x: quantize(ggml_type, x, q)
+        # a CPU (or MPS) kernel: its imatrix goes to the ROCm device once, on
+        # first use, instead of once per call
+        staged = {}
+
+        def quant_fn(x):
+            if x.device.type == "cuda":
+                return quantize(ggml_type, x, q.to(x.device))
+            if "q" not in staged:
+                staged["q"] = q.to(_rocm_device())
+            got = quantize(ggml_type, x.to(staged["q"].device), staged["q"])
+            return got.to(x.device)
+        return quant_fn
     return make_kernel
 
 
@@ -242,4 +318,5 @@ def _registry() -> dict[str, QuantSpec]:
 QUANT_TYPES: dict[str, QuantSpec] = _registry()
 
 __all__ = ["QUANT_TYPES", "ALL_SPECS", "QuantSpec", "QuantSpecError", "TORCH_DTYPES",
-           "GGMLQuantizationType", "LlamaFileType", "library", "quantize", "row_bytes"]
+           "GGMLQuantizationType", "LlamaFileType", "library", "quantize", "row_bytes", "init",
+           "set_sqrt_rounding", "sqrt_rounding"]

@@ -32,16 +32,18 @@ SOURCES = ["qs_api.hip", "qs_pipeline.cpp"]
 
 
 def build(verbose: bool = False) -> Path:
-    _compile(OUT, SOURCES, verbose)
+    # the AMD-host square-root map is embedded in the library (.incbin)
+    _compile(OUT, SOURCES, verbose, [f'-DQS_SQRT_AMD_BIN="{CSRC / "qs_sqrt_amd.bin"}"'], ["-lz"])
     _compile(CALIB_OUT, ["qs_calib.hip"], verbose)
     return OUT
 
 
-def _compile(out: Path, sources: list[str], verbose: bool) -> None:
+def _compile(out: Path, sources: list[str], verbose: bool, defines: list[str] | None = None,
+             libs: list[str] | None = None) -> None:
     out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_name(out.name + ".tmp")
-    cmd = [HIPCC, *FLAGS, f"-I{ROOT / 'include'}", f"-I{CSRC}", "-o", str(tmp),
-           *[str(CSRC / s) for s in sources]]
+    cmd = [HIPCC, *FLAGS, *(defines or []), f"-I{ROOT / 'include'}", f"-I{CSRC}", "-o", str(tmp),
+           *[str(CSRC / s) for s in sources], *(libs or [])]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -5,13 +5,18 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
+#include <utility>
 #include <vector>
+
+#include <zlib.h>
 
 #include "quant_studio.h"
 #include "qs_grids.h"
@@ -23,6 +28,26 @@
 namespace {
 thread_local std::string g_err;
 }  // namespace
+
+// The AMD-host square-root map (qs_sqrt_amd.bin: zlib-compressed, 2 bits per
+// key, written by gen_sqrt_table.py --write-map on an AMD EPYC host),
+// embedded at build time. Host code only.
+#ifndef QS_SQRT_AMD_BIN
+#error "build with -DQS_SQRT_AMD_BIN=<path of qs_sqrt_amd.bin> (quant-studio_amd/build.py)"
+#endif
+#if !defined(__HIP_DEVICE_COMPILE__)
+__asm__(".section .rodata\n"
+        ".balign 16\n"
+        ".global qs_sqrt_amd_blob\n"
+        ".hidden qs_sqrt_amd_blob\n"
+        "qs_sqrt_amd_blob:\n"
+        ".incbin \"" QS_SQRT_AMD_BIN "\"\n"
+        ".global qs_sqrt_amd_blob_end\n"
+        ".hidden qs_sqrt_amd_blob_end\n"
+        "qs_sqrt_amd_blob_end:\n"
+        ".previous\n");
+#endif
+extern "C" const unsigned char qs_sqrt_amd_blob[], qs_sqrt_amd_blob_end[];
 
 namespace qs_host {
 
@@ -182,25 +207,51 @@ int iq_table_of(int ggml_type) {
 }
 
 std::mutex g_dev_mutex;
+
+// Square-root maps (2^24 bits each, see qs::SqrtMap): the Intel-host set that
+// torch.sqrt rounds one ulp down (qs_sqrt_table.h), and the AMD-host sets
+// rounded one ulp down and one ulp up (qs_sqrt_amd.bin).
+enum SqrtMapId { SQM_INTEL_DOWN, SQM_AMD_DOWN, SQM_AMD_UP, SQM_N };
+
+// lookup bands of the two hosts' maps, in units of r * ulp(r) (qs::SqrtMap;
+// both proven over all 2^24 keys by the tests)
+constexpr float kIntelBandLo = -0.875f;
+constexpr float kAmdBand = 0.48f;
+
 // Per-device constant tables: the IQ grids and neighbour lists, and the
-// square-root map of sqrt_ref (2^24 bits expanded from qs_sqrt_table.h).
+// square-root maps.
 struct DevTables {
     std::array<qs::IqTabDev, IQT_N> iq{};
-    const uint32_t* sqrt_down = nullptr;
+    std::array<const uint32_t*, SQM_N> sqrt{};
 };
 
-const std::vector<uint32_t>& sqrt_down_bits() {
+// the three maps, expanded on the host once per process (false if the
+// embedded AMD map is corrupt)
+bool sqrt_map_bits(std::array<std::vector<uint32_t>, SQM_N>*& out) {
     static std::once_flag once;
-    static std::vector<uint32_t> bits;
+    static std::array<std::vector<uint32_t>, SQM_N> bits;
+    static bool ok = false;
     std::call_once(once, [] {
-        bits.assign(1u << 19, 0u);
+        for (auto& b : bits) b.assign(1u << 19, 0u);
         uint32_t key = 0;
         for (int i = 0; i < QS_SQRT_DOWN_N; i++) {
             key += QS_SQRT_DOWN_GAPS[i];
-            bits[key >> 5] |= 1u << (key & 31u);
+            bits[SQM_INTEL_DOWN][key >> 5] |= 1u << (key & 31u);
         }
+        std::vector<unsigned char> packed(1u << 22);
+        uLongf len = (uLongf)packed.size();
+        const uLong clen = (uLong)(qs_sqrt_amd_blob_end - qs_sqrt_amd_blob);
+        if (uncompress(packed.data(), &len, qs_sqrt_amd_blob, clen) != Z_OK || len != packed.size())
+            return;
+        for (uint32_t k = 0; k < (1u << 24); k++) {
+            const uint32_t code = (packed[k >> 2] >> (2 * (k & 3u))) & 3u;
+            if (code == 3) return;
+            if (code) bits[code == 1 ? SQM_AMD_DOWN : SQM_AMD_UP][k >> 5] |= 1u << (k & 31u);
+        }
+        ok = true;
     });
-    return bits;
+    out = &bits;
+    return ok;
 }
 
 template <typename T>
@@ -213,18 +264,27 @@ const T* upload(const std::vector<T>& v) {
     return static_cast<const T*>(p);
 }
 
-// Tables of the current device, uploaded on first use (an IQ grid's tables
-// when a type using that grid first runs) and kept until the process ends.
+// Tables of each device, uploaded on first use (an IQ grid's tables when a
+// type using that grid first runs, or all of them by qs_init) and kept until
+// the process ends.
 std::map<int, DevTables> g_dev_state;
 
-bool device_tables(int iq_table, DevTables& out) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return false;
-    std::lock_guard<std::mutex> lock(g_dev_mutex);
+// square-root rounding of the weights (QS_SQRT_*), process-wide
+std::atomic<int> g_sqrt_mode{QS_SQRT_TORCH_CPU};
+
+// the maps a square-root mode reads
+std::array<bool, SQM_N> maps_of(int mode) {
+    return {mode == QS_SQRT_TORCH_CPU, mode == QS_SQRT_TORCH_CPU_AMD, mode == QS_SQRT_TORCH_CPU_AMD};
+}
+
+bool device_tables_locked(int dev, int iq_table, const std::array<bool, SQM_N>& maps, DevTables& out) {
     DevTables& d = g_dev_state[dev];
-    if (!d.sqrt_down) {
-        d.sqrt_down = upload(sqrt_down_bits());
-        if (!d.sqrt_down) return false;
+    for (int m = 0; m < SQM_N; m++) {
+        if (!maps[m] || d.sqrt[m]) continue;
+        std::array<std::vector<uint32_t>, SQM_N>* bits = nullptr;
+        if (!sqrt_map_bits(bits)) return false;
+        d.sqrt[m] = upload((*bits)[m]);
+        if (!d.sqrt[m]) return false;
     }
     if (iq_table >= 0 && !d.iq[iq_table].grid) {
         const HostTab& h = host_tab(iq_table);
@@ -238,6 +298,39 @@ bool device_tables(int iq_table, DevTables& out) {
     }
     out = d;
     return true;
+}
+
+// tables of the current device (uploaded under the lock when missing)
+bool device_tables(int iq_table, int sqrt_mode, DevTables& out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::lock_guard<std::mutex> lock(g_dev_mutex);
+    return device_tables_locked(dev, iq_table, maps_of(sqrt_mode), out);
+}
+
+// the kernels' view of a square-root mode
+qs::SqrtMap sqrt_map(int mode, const DevTables& t) {
+    qs::SqrtMap m{};
+    const float inf = __builtin_inff();
+    if (mode == QS_SQRT_TORCH_CPU) m = {t.sqrt[SQM_INTEL_DOWN], nullptr, kIntelBandLo, inf};
+    else if (mode == QS_SQRT_TORCH_CPU_AMD) m = {t.sqrt[SQM_AMD_DOWN], t.sqrt[SQM_AMD_UP], -kAmdBand, kAmdBand};
+    else m = {nullptr, nullptr, 0.0f, 0.0f};      // QS_SQRT_IEEE
+    return m;
+}
+
+// Launch through hipLaunchKernel so its status comes back as the return
+// value: the caller's pending hipGetLastError() state is neither read nor
+// reset by this library.
+template <typename... P, typename... A>
+hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t st, A&&... args) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    std::tuple<P...> vals(std::forward<A>(args)...);
+    void* argv[sizeof...(P)];
+    std::apply([&](auto&... v) {
+        int i = 0;
+        ((argv[i++] = static_cast<void*>(&v)), ...);
+    }, vals);
+    return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, 0, st);
 }
 
 qs::IqSteps iq_steps(float base, float delta, int lo, int hi) {
@@ -286,60 +379,52 @@ qs::Steps qx_steps(int nmax) {
 }
 
 template <int SRC, qs::B32 T>
-void launch_b32(const qs::KArgs& a, hipStream_t st) {
+hipError_t launch_b32(const qs::KArgs& a, hipStream_t st) {
     const unsigned g = (unsigned)((a.n_units + qs::Q40_BLOCKS_PER_WG - 1) / qs::Q40_BLOCKS_PER_WG);
-    hipLaunchKernelGGL((qs::k_b32<SRC, T>), dim3(g), dim3(256), 0, st, a);
+    return launch(qs::k_b32<SRC, T>, dim3(g), dim3(256), st, a);
 }
 
 template <int SRC>
-void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
-                 const std::array<qs::IqTabDev, IQT_N>& tabs) {
+hipError_t launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
+                       const std::array<qs::IqTabDev, IQT_N>& tabs) {
     using namespace qs;
-    const unsigned sb8 = (unsigned)((a.n_units + 7) / 8), sb4 = (unsigned)((a.n_units + 3) / 4);
+    const dim3 wave(64);
+    const dim3 sb8((unsigned)((a.n_units + 7) / 8)), sb4((unsigned)((a.n_units + 3) / 4));
     switch (type) {
-    case QS_TYPE_Q4_0: launch_b32<SRC, B32::Q4_0>(a, st); break;
-    case QS_TYPE_Q4_1: launch_b32<SRC, B32::Q4_1>(a, st); break;
-    case QS_TYPE_Q5_0: launch_b32<SRC, B32::Q5_0>(a, st); break;
-    case QS_TYPE_Q5_1: launch_b32<SRC, B32::Q5_1>(a, st); break;
-    case QS_TYPE_Q8_0: launch_b32<SRC, B32::Q8_0>(a, st); break;
+    case QS_TYPE_Q4_0: return launch_b32<SRC, B32::Q4_0>(a, st);
+    case QS_TYPE_Q4_1: return launch_b32<SRC, B32::Q4_1>(a, st);
+    case QS_TYPE_Q5_0: return launch_b32<SRC, B32::Q5_0>(a, st);
+    case QS_TYPE_Q5_1: return launch_b32<SRC, B32::Q5_1>(a, st);
+    case QS_TYPE_Q8_0: return launch_b32<SRC, B32::Q8_0>(a, st);
     case QS_TYPE_IQ4_NL: {
-        const unsigned g = (unsigned)((a.n_units + 63) / 64);
-        if (imat) hipLaunchKernelGGL((k_iq4_nl<SRC, true>), dim3(g), dim3(64), 0, st, a);
-        else hipLaunchKernelGGL((k_iq4_nl<SRC, false>), dim3(g), dim3(64), 0, st, a);
-        break;
+        const dim3 g((unsigned)((a.n_units + 63) / 64));
+        return imat ? launch(k_iq4_nl<SRC, true>, g, wave, st, a)
+                    : launch(k_iq4_nl<SRC, false>, g, wave, st, a);
     }
     case QS_TYPE_Q4_K:
-        if (imat) hipLaunchKernelGGL((k_q45_k<SRC, true, 15>), dim3(sb8), dim3(64), 0, st, a,
-                                     qkx_steps(-0.9f, 0.05f, 36, 15), qp_steps(63));
-        else hipLaunchKernelGGL((k_q45_k<SRC, false, 15>), dim3(sb8), dim3(64), 0, st, a,
-                                qkx_steps(-1.0f, 0.1f, 20, 15), qp_steps(63));
-        break;
+        return imat ? launch(k_q45_k<SRC, true, 15>, sb8, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 15),
+                             qp_steps(63))
+                    : launch(k_q45_k<SRC, false, 15>, sb8, wave, st, a, qkx_steps(-1.0f, 0.1f, 20, 15),
+                             qp_steps(63));
     case QS_TYPE_Q5_K:
-        if (imat) hipLaunchKernelGGL((k_q45_k<SRC, true, 31>), dim3(sb8), dim3(64), 0, st, a,
-                                     qkx_steps(-0.9f, 0.05f, 36, 31), qp_steps(63));
-        else hipLaunchKernelGGL((k_q45_k<SRC, false, 31>), dim3(sb8), dim3(64), 0, st, a,
-                                qkx_steps(-0.5f, 0.1f, 15, 31), qp_steps(63));
-        break;
+        return imat ? launch(k_q45_k<SRC, true, 31>, sb8, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 31),
+                             qp_steps(63))
+                    : launch(k_q45_k<SRC, false, 31>, sb8, wave, st, a, qkx_steps(-0.5f, 0.1f, 15, 31),
+                             qp_steps(63));
     case QS_TYPE_Q6_K:
-        if (imat) hipLaunchKernelGGL((k_q6_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a, qx_steps(32));
-        else hipLaunchKernelGGL((k_q6_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a, qx_steps(32));
-        break;
+        return imat ? launch(k_q6_k<SRC, true>, sb4, wave, st, a, qx_steps(32))
+                    : launch(k_q6_k<SRC, false>, sb4, wave, st, a, qx_steps(32));
     case QS_TYPE_Q3_K:
-        if (imat) hipLaunchKernelGGL((k_q3_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a, qx_steps(4),
-                                     qx_steps(32));
-        else hipLaunchKernelGGL((k_q3_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a, qx_steps(4),
-                                qx_steps(32));
-        break;
+        return imat ? launch(k_q3_k<SRC, true>, sb4, wave, st, a, qx_steps(4), qx_steps(32))
+                    : launch(k_q3_k<SRC, false>, sb4, wave, st, a, qx_steps(4), qx_steps(32));
     case QS_TYPE_Q2_K:
-        if (imat) hipLaunchKernelGGL((k_q2_k<SRC, true>), dim3(sb4), dim3(64), 0, st, a,
-                                     qkx_steps(-0.9f, 0.05f, 36, 3), qp_steps(15));
-        else hipLaunchKernelGGL((k_q2_k<SRC, false>), dim3(sb4), dim3(64), 0, st, a,
-                                qkx_steps(-0.5f, 0.1f, 15, 3), qp_steps(15));
-        break;
+        return imat ? launch(k_q2_k<SRC, true>, sb4, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 3),
+                             qp_steps(15))
+                    : launch(k_q2_k<SRC, false>, sb4, wave, st, a, qkx_steps(-0.5f, 0.1f, 15, 3),
+                             qp_steps(15));
     case QS_TYPE_IQ4_XS:
-        if (imat) hipLaunchKernelGGL((k_iq4_xs<SRC, true>), dim3(sb8), dim3(64), 0, st, a);
-        else hipLaunchKernelGGL((k_iq4_xs<SRC, false>), dim3(sb8), dim3(64), 0, st, a);
-        break;
+        return imat ? launch(k_iq4_xs<SRC, true>, sb8, wave, st, a)
+                    : launch(k_iq4_xs<SRC, false>, sb8, wave, st, a);
     case QS_TYPE_IQ2_XXS: {
         // candidate numerators computed in f64 and rounded once (iq2.py:387, :470)
         QpSteps qp4{};
@@ -348,29 +433,24 @@ void launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
         for (int i = -4; i <= 4; i++)
             if (i) qp4.v[n++] = (float)(0.1 * i + 4.0);
         for (int i = -6; i <= 6; i++) sweep.v[sweep.n++] = (float)(5.0 + 0.1 * i);
-        hipLaunchKernelGGL(k_iq2_xxs<SRC>, dim3(sb8), dim3(64), 0, st, a, tabs[IQT_G2_256], qp4, sweep);
-        break;
+        return launch(k_iq2_xxs<SRC>, sb8, wave, st, a, tabs[IQT_G2_256], qp4, sweep);
     }
     case QS_TYPE_IQ2_XS:      // SWEEP_CS iq2xs_common.py:21
-        hipLaunchKernelGGL((k_iq2_xs_s<SRC, false>), dim3(sb4), dim3(64), 0, st, a, tabs[IQT_G2_512],
-                           iq_steps(5.0f, 0.1f, -9, 9));
-        break;
+        return launch(k_iq2_xs_s<SRC, false>, sb4, wave, st, a, tabs[IQT_G2_512],
+                      iq_steps(5.0f, 0.1f, -9, 9));
     case QS_TYPE_IQ2_S:
-        hipLaunchKernelGGL((k_iq2_xs_s<SRC, true>), dim3(sb4), dim3(64), 0, st, a, tabs[IQT_G2_1024],
-                           iq_steps(5.0f, 0.1f, -9, 9));
-        break;
+        return launch(k_iq2_xs_s<SRC, true>, sb4, wave, st, a, tabs[IQT_G2_1024],
+                      iq_steps(5.0f, 0.1f, -9, 9));
     case QS_TYPE_IQ3_XXS:     // _STEPS iq3_xxs.py:22
-        hipLaunchKernelGGL((k_iq3<SRC, false, true>), dim3(sb8), dim3(64), 0, st, a, tabs[IQT_G3_256],
-                           iq_steps(15.0f, 0.2f, -15, 15));
-        break;
+        return launch(k_iq3<SRC, false, true>, sb8, wave, st, a, tabs[IQT_G3_256],
+                      iq_steps(15.0f, 0.2f, -15, 15));
     case QS_TYPE_IQ3_S:       // _STEPS iq3_s.py:22
-        if (imat) hipLaunchKernelGGL((k_iq3<SRC, true, true>), dim3(sb8), dim3(64), 0, st, a,
-                                     tabs[IQT_G3_512], iq_steps(15.0f, 0.2f, -9, 9));
-        else hipLaunchKernelGGL((k_iq3<SRC, true, false>), dim3(sb8), dim3(64), 0, st, a,
-                                tabs[IQT_G3_512], iq_steps(15.0f, 0.2f, -9, 9));
-        break;
+        return imat ? launch(k_iq3<SRC, true, true>, sb8, wave, st, a, tabs[IQT_G3_512],
+                             iq_steps(15.0f, 0.2f, -9, 9))
+                    : launch(k_iq3<SRC, true, false>, sb8, wave, st, a, tabs[IQT_G3_512],
+                             iq_steps(15.0f, 0.2f, -9, 9));
     default:
-        break;
+        return hipErrorInvalidValue;
     }
 }
 
@@ -450,18 +530,51 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     a.dst = static_cast<uint8_t*>(dst);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     DevTables tabs;
-    if (!device_tables(iq_table_of(ggml_type), tabs))
+    const int mode = g_sqrt_mode.load(std::memory_order_relaxed);
+    if (!device_tables(iq_table_of(ggml_type), mode, tabs))
         return fail(QS_EIO, "%s: cannot upload constant tables to the device", t->name);
-    a.sqrt_down = tabs.sqrt_down;
-    (void)hipGetLastError();
+    a.sqrt = sqrt_map(mode, tabs);
+    hipError_t e;
     switch (src_type) {
-    case QS_SRC_F32: launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs.iq); break;
-    case QS_SRC_F16: launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs.iq); break;
-    default: launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs.iq); break;
+    case QS_SRC_F32: e = launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs.iq); break;
+    case QS_SRC_F16: e = launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs.iq); break;
+    default: e = launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs.iq); break;
     }
-    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(QS_EIO, "%s: launch failed: %s", t->name, hipGetErrorString(e));
     return 0;
 }
+
+int qs_init(int device) {
+    g_err.clear();
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n)
+        return fail(QS_EINVAL, "device %d not present (%d ROCm devices)", device, n);
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return fail(QS_EIO, "hipGetDevice failed");
+    if (hipSetDevice(device) != hipSuccess) return fail(QS_EIO, "hipSetDevice(%d) failed", device);
+    bool ok = true;
+    {
+        std::lock_guard<std::mutex> lock(g_dev_mutex);
+        DevTables d;
+        const std::array<bool, SQM_N> all{true, true, true};
+        for (int id = 0; id < IQT_N && ok; id++) ok = device_tables_locked(device, id, all, d);
+    }
+    // the uploads are blocking copies: nothing of this library is pending on
+    // the device when qs_init returns
+    const bool restored = hipSetDevice(prev) == hipSuccess;
+    if (!ok) return fail(QS_EIO, "cannot upload constant tables to device %d", device);
+    if (!restored) return fail(QS_EIO, "hipSetDevice(%d) failed", prev);
+    return 0;
+}
+
+int qs_set_sqrt_rounding(int mode) {
+    if (mode != QS_SQRT_TORCH_CPU && mode != QS_SQRT_IEEE && mode != QS_SQRT_TORCH_CPU_AMD)
+        return fail(QS_EINVAL, "square-root mode %d (torch CPU Intel = %d, IEEE = %d, torch CPU AMD = %d)",
+                    mode, QS_SQRT_TORCH_CPU, QS_SQRT_IEEE, QS_SQRT_TORCH_CPU_AMD);
+    g_sqrt_mode.store(mode, std::memory_order_relaxed);
+    return 0;
+}
+
+int qs_get_sqrt_rounding(void) { return g_sqrt_mode.load(std::memory_order_relaxed); }
 
 }  // extern "C"

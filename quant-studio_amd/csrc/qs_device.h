@@ -9,8 +9,9 @@
 //   - torch's `python_float / tensor` is `tensor.reciprocal() * float`
 //     (two roundings), which rdiv() restates;
 //   - torch.round is round-half-even: rintf -> v_rndne_f32;
-//   - torch.sqrt on a CPU tensor is not correctly rounded: sqrt_ref() is the
-//     IEEE root minus one ulp on the tabulated set where torch rounds down.
+//   - torch.sqrt on a CPU tensor is not correctly rounded, and how it rounds
+//     depends on the host's MKL: sqrt_ref() is the IEEE root adjusted by one
+//     ulp on the tabulated keys of the selected host (or left IEEE).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -53,82 +54,113 @@ QS_DEV void keep_in_registers(float (&v)[N]) {
     for (int i = 0; i < N; i++) keep_in_register(v[i]);
 }
 
-// The reference's square root (torch.sqrt on CPU, kernels/q4_k.py:34, :51,
-// iq2.py:431, :436 and the other weight sites): the IEEE root, one ulp lower
-// when the input's key (exponent parity << 23 | mantissa, subnormals scaled
-// by 2^64 first) is set in `down`, a 2^24-bit map built per device from
-// qs_sqrt_table.h. Zero, negative, infinite and NaN inputs keep the IEEE result.
+// The reference's square root (torch.sqrt, kernels/q4_k.py:34, :51,
+// iq2.py:431, :436 and the other weight sites), whose rounding depends on the
+// host it ran on. SqrtMap selects it:
+//   down == nullptr: the IEEE root (torch.sqrt on a GPU tensor, C sqrtf);
+//   else the IEEE root, one ulp lower where the input's key is set in `down`
+//   and one ulp higher where it is set in `up` (nullptr: never), with the key
+//   (exponent parity << 23 | mantissa, subnormals scaled by 2^64 first)
+//   indexing two 2^24-bit maps built per device from the measured tables.
+// The maps are read only where the exact root s can lie on the flipped side:
+// with r the IEEE root and rem = v - r^2 (exact, fma(-r, r, v)),
+// s - r = rem / (s + r), and every tabulated key has rem below band_lo * r *
+// ulp(r) (down) or above band_hi * r * ulp(r) (up), checked over all 2^24 keys
+// on the host; below 2^-80 the products lose precision and the map is always
+// read. Zero, negative, infinite and NaN inputs keep the IEEE result. Lanes
+// that need no lookup read word 0 (one shared cache line).
+struct SqrtMap {
+    const uint32_t* down;
+    const uint32_t* up;
+    float band_lo, band_hi;
+};
+
 QS_DEV uint32_t sqrt_key(float v) {
     const uint32_t b = __float_as_uint(v);
     const uint32_t bn = b < 0x00800000u ? __float_as_uint(v * 18446744073709551616.0f) : b;
     return ((((bn >> 23) & 1u) ^ 1u) << 23) | (bn & 0x7fffffu);     // always < 2^24
 }
 
-// Every input the map lists has its exact root s within 0.0601 ulp above the
-// midpoint below the IEEE root r (checked over all 2^24 keys on the host), so
-// the map needs reading only where s - r < -7/16 ulp(r); that is about 6% of
-// inputs, and the other lanes read word 0 (one shared cache line) instead of
-// a scattered one. fma(-r, r, v) is the exact remainder v - r^2, and
-// s - r = (v - r^2) / (s + r), so the test is (v - r^2) < -0.875 r ulp(r).
-// Below 2^-80 the products lose precision and the map is always read.
-// Returns the map key with bit 31 set when the map must be read, else 0
-// (zero, negative, infinite and NaN inputs never are).
-QS_DEV uint32_t sqrt_lookup_key(float v, float r) {
+// The map key with bit 31 set when the maps must be read for v (root r), else 0.
+QS_DEV uint32_t sqrt_lookup_key(float v, float r, const SqrtMap& m) {
     const float rem = __builtin_fmaf(-r, r, v);
     const float ulp = __uint_as_float((__float_as_uint(r) & 0x7f800000u) - (23u << 23));
-    const float lim = (-0.875f * r) * ulp;
+    const float lim_lo = (m.band_lo * r) * ulp, lim_hi = (m.band_hi * r) * ulp;
     const uint32_t b = __float_as_uint(v);
-    const bool look = (b - 1u < 0x7f7fffffu) && (rem < lim || b < 0x17800000u);
+    const bool look = (b - 1u < 0x7f7fffffu) && (rem < lim_lo || rem > lim_hi || b < 0x17800000u);
     return look ? (sqrt_key(v) | 0x80000000u) : 0u;
 }
 
-// r minus one ulp when the looked-up map bit is set
-QS_DEV float sqrt_fix(float r, uint32_t kn, uint32_t word) {
-    const uint32_t dn = (kn >> 31) & (word >> (kn & 31u));
-    return __uint_as_float(__float_as_uint(r) - dn);
+// r adjusted by the looked-up map bits (kn from sqrt_lookup_key)
+QS_DEV float sqrt_fix(float r, uint32_t kn, uint32_t wdown, uint32_t wup) {
+    const uint32_t sh = kn & 31u, on = kn >> 31;
+    const uint32_t dn = on & (wdown >> sh), up = on & (wup >> sh);
+    return __uint_as_float(__float_as_uint(r) - (dn & 1u) + (up & 1u));
 }
 
-QS_DEV const uint32_t* sqrt_word(const uint32_t* __restrict__ down, uint32_t kn) {
-    return down + ((kn & 0x00ffffffu) >> 5);
+QS_DEV uint32_t sqrt_word(const uint32_t* __restrict__ map, uint32_t kn) {
+    return map[(kn & 0x00ffffffu) >> 5];
 }
 
-// r = sqrtf(v), one ulp lower when the input's map bit is set (every input
-// reads its own word)
-QS_DEV float sqrt_fix_plain(float v, uint32_t key, uint32_t word) {
+// r = sqrtf(v) adjusted by the key's bits when every input reads its own words
+QS_DEV float sqrt_fix_plain(float v, uint32_t key, uint32_t wdown, uint32_t wup) {
     const float r = sqrtf(v);
-    const bool dn = (__float_as_uint(v) - 1u < 0x7f7fffffu) && ((word >> (key & 31u)) & 1u);
-    return dn ? __uint_as_float(__float_as_uint(r) - 1u) : r;
+    const uint32_t on = (__float_as_uint(v) - 1u < 0x7f7fffffu) ? 1u : 0u;
+    const uint32_t dn = on & (wdown >> (key & 31u)), up = on & (wup >> (key & 31u));
+    return __uint_as_float(__float_as_uint(r) - (dn & 1u) + (up & 1u));
 }
 
-QS_DEV float sqrt_ref(float v, const uint32_t* __restrict__ down) {
+// The test on the map pointers is on kernel arguments, so every branch on
+// them is uniform.
+QS_DEV float sqrt_ref(float v, const SqrtMap& m) {
+    if (!m.down) return sqrtf(v);
     const uint32_t key = sqrt_key(v);
-    return sqrt_fix_plain(v, key, down[key >> 5]);
+    return sqrt_fix_plain(v, key, m.down[key >> 5], m.up ? m.up[key >> 5] : 0u);
 }
 
 // sqrt_ref over a lane's N values, every map load issued before any is used.
-// BAND reads the map only near midpoints (sqrt_lookup_key); without it every
-// value reads its own word, which keeps fewer registers live: the Q4_K/Q5_K
+// BAND reads the maps only where sqrt_lookup_key asks; without it every value
+// reads its own words, which keeps fewer registers live: the Q4_K/Q5_K
 // kernels measured 1-2% faster that way, the others 2-17% slower.
 template <int N, bool BAND = true>
-QS_DEV void sqrt_ref_n(const float (&v)[N], const uint32_t* __restrict__ down, float (&out)[N]) {
-    uint32_t kn[N], word[N];
+QS_DEV void sqrt_ref_n(const float (&v)[N], const SqrtMap& m, float (&out)[N]) {
+    if (!m.down) {
+#pragma unroll
+        for (int i = 0; i < N; i++) out[i] = sqrtf(v[i]);
+        return;
+    }
+    uint32_t kn[N], wd[N], wu[N];
     if constexpr (BAND) {
 #pragma unroll
         for (int i = 0; i < N; i++) {
             out[i] = sqrtf(v[i]);
-            kn[i] = sqrt_lookup_key(v[i], out[i]);
+            kn[i] = sqrt_lookup_key(v[i], out[i], m);
         }
 #pragma unroll
-        for (int i = 0; i < N; i++) word[i] = *sqrt_word(down, kn[i]);
+        for (int i = 0; i < N; i++) wd[i] = sqrt_word(m.down, kn[i]);
+        if (m.up) {
 #pragma unroll
-        for (int i = 0; i < N; i++) out[i] = sqrt_fix(out[i], kn[i], word[i]);
+            for (int i = 0; i < N; i++) wu[i] = sqrt_word(m.up, kn[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; i++) wu[i] = 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++) out[i] = sqrt_fix(out[i], kn[i], wd[i], wu[i]);
     } else {
 #pragma unroll
         for (int i = 0; i < N; i++) kn[i] = sqrt_key(v[i]);
 #pragma unroll
-        for (int i = 0; i < N; i++) word[i] = down[kn[i] >> 5];
+        for (int i = 0; i < N; i++) wd[i] = m.down[kn[i] >> 5];
+        if (m.up) {
 #pragma unroll
-        for (int i = 0; i < N; i++) out[i] = sqrt_fix_plain(v[i], kn[i], word[i]);
+            for (int i = 0; i < N; i++) wu[i] = m.up[kn[i] >> 5];
+        } else {
+#pragma unroll
+            for (int i = 0; i < N; i++) wu[i] = 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++) out[i] = sqrt_fix_plain(v[i], kn[i], wd[i], wu[i]);
     }
 }
 
@@ -136,7 +168,7 @@ QS_DEV void sqrt_ref_n(const float (&v)[N], const uint32_t* __restrict__ down, f
 // with the imatrix and map loads issued together
 template <int N, bool BAND = true>
 QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const float (&x)[N],
-                            const uint32_t* __restrict__ down, float (&w)[N]) {
+                            const SqrtMap& m, float (&w)[N]) {
     float v[N], q[N];
 #pragma unroll
     for (int i = 0; i < N; i++) {
@@ -145,7 +177,7 @@ QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const fl
         q[i] = qw[i];
     }
     float r[N];
-    sqrt_ref_n<N, BAND>(v, down, r);
+    sqrt_ref_n<N, BAND>(v, m, r);
 #pragma unroll
     for (int i = 0; i < N; i++) w[i] = q[i] * r[i];
 }

@@ -425,7 +425,7 @@ QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K],
     }
     const float sum = sb_sumsq_halves<LPS, SPW, GROUP>(vlds, tmp, x, p.slot, p.g);
     const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
-    imatrix_weights<GROUP>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
+    imatrix_weights<GROUP>(a.qw + p.col, sigma2, x, a.sqrt, w);
 }
 
 // ------------------------------------------------------------------
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
     iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 1.0f, false, x, w);
-    sqrt_ref_n<32>(w, a.sqrt_down, waux);
+    sqrt_ref_n<32>(w, a.sqrt, waux);
     keep_in_registers(waux);
     int signs[4];
     static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
@@ -553,7 +553,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
     iq_load_weights<SRC, LPS, 16>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
-    sqrt_ref_n<16>(w, a.sqrt_down, waux);
+    sqrt_ref_n<16>(w, a.sqrt, waux);
     int signs[2];
     if constexpr (IS_S) {
         signs[0] = sign_bits8<0>(x, xval);
@@ -685,7 +685,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
     iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
-    sqrt_ref_n<32>(w, a.sqrt_down, waux);
+    sqrt_ref_n<32>(w, a.sqrt, waux);
     keep_in_registers(waux);
     int signs[4];
     if constexpr (IS_S) {

@@ -24,7 +24,7 @@ struct KArgs {
     int64_t stride;       // source row stride in elements
     const float* qw;      // k imatrix weights or nullptr
     uint8_t* dst;         // packed output, n_units * block bytes
-    const uint32_t* sqrt_down;   // sqrt_ref's 2^24-bit map (device copy)
+    SqrtMap sqrt;         // square-root rounding of the weights (sqrt_ref)
 };
 
 struct QpSteps {
@@ -176,7 +176,11 @@ QS_DEV void b32_block(const float (&x)[8], int q, uint8_t* o) {
         uint32_t w[2] = {0u, 0u};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const int v = (int)roundf(x[i] * id);
+            // where 1/d overflowed (d below 127 * 2^-128) x * id is infinite or
+            // NaN: saturate to [-128, 127], NaN to 0, instead of an undefined
+            // conversion
+            const float r = roundf(x[i] * id);
+            const int v = r == r ? (int)clampf(r, -128.0f, 127.0f) : 0;
             w[i >> 2] |= ((uint32_t)v & 0xffu) << (8 * (i & 3));
         }
         if (q == 0) o16[0] = (uint16_t)f16_bits(d);
@@ -324,12 +328,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4
         wave_sync();
         const float sum = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g);
         const float sigma2 = (2.0f * sum) / 256.0f;
-        imatrix_weights<32, false>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
+        imatrix_weights<32, false>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
         float t[32];
 #pragma unroll
         for (int i = 0; i < 32; i++) t[i] = x[i] * x[i];
-        const float av = sqrt_ref(cascade8_sum(t) / 32.0f, a.sqrt_down);
+        const float av = sqrt_ref(cascade8_sum(t) / 32.0f, a.sqrt);
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = av + fabsf(x[i]);
     }
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps3
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = (2.0f * sb_seq_256(s.v[slot])) / 256.0f;
-        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
+        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt, w);
         const QxResult r = qx_fit<16>(x, w, 4, steps4);
 #pragma unroll
         for (int i = 0; i < 16; i++) Lg[i] = qx_level(r, x[i], 4.0f);
@@ -639,7 +643,7 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g) / 256.0f;
-        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
+        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt, w);
         r = qkx_fit<16, false>(x, w, steps, 3.0f);
         s.sc[slot][g] = r.scale;
         s.mn[slot][g] = r.the_min;
@@ -726,7 +730,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, p.elem, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW, 32>(s.v, s.tmp, x, slot, g)) / 256.0f;
-        imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt_down, w);
+        imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
@@ -802,7 +806,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, row * a.stride + col, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * cascade8_of<32>([&](int i) { return x[i] * x[i]; })) / 32.0f;
-        imatrix_weights<32>(a.qw + col, sigma2, x, a.sqrt_down, w);
+        imatrix_weights<32>(a.qw + col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];

@@ -280,24 +280,28 @@ def write_gguf(path: str | Path, arch: str, kvs: list[KV],
 
 
 def load_imatrix(path: str | Path) -> dict[str, np.ndarray]:
-    """Per-tensor imatrix weights: mean squared input activation per column,
-    `<name>.in_sum2` divided by `<name>.counts` (0 where the count is 0), one
-    block of values per count (per expert)."""
-    r = GGUFReader(path)
-    sums, counts = {}, {}
-    for t in r.tensors:
-        if t.name.endswith(".in_sum2"):
-            sums[t.name[:-len(".in_sum2")]] = np.array(t.data.view(np.float32), copy=True)
-        elif t.name.endswith(".counts"):
-            counts[t.name[:-len(".counts")]] = np.array(t.data.view(np.float32), copy=True)
-    out = {}
-    for name, s in sums.items():
-        c = counts.get(name)
-        if c is None:
+    """Per-tensor imatrix weights from a GGUF imatrix file (the format of
+    load_imatrix, quant-studio.py:68-87): for each tensor name with both a
+    `<name>.in_sum2` and a `<name>.counts` record, the mean squared input
+    activation per column, in_sum2 / counts in float32 -- one row of values per
+    count (per expert for 3-D tensors), 0 where that count is not positive --
+    flattened in row order."""
+    records: dict[str, dict[str, np.ndarray]] = {}
+    reader = GGUFReader(path)
+    try:
+        for t in reader.tensors:
+            base, _, field = t.name.rpartition(".")
+            if base and field in ("in_sum2", "counts"):
+                records.setdefault(base, {})[field] = np.array(t.data.view(np.float32), copy=True)
+    finally:
+        reader.close()
+    weights = {}
+    for base, rec in records.items():
+        if "in_sum2" not in rec or "counts" not in rec:
             continue
-        e = s.reshape(c.size, -1)
-        w = np.zeros_like(e)
-        np.divide(e, c[:, None], out=w, where=c[:, None] > 0)
-        out[name] = w.reshape(-1)
-    r.close()
-    return out
+        counts = rec["counts"].reshape(-1, 1)
+        per_count = rec["in_sum2"].reshape(counts.shape[0], -1)
+        live = counts > 0
+        mean = per_count / np.where(live, counts, np.float32(1))
+        weights[base] = np.where(live, mean, np.float32(0)).astype(np.float32).reshape(-1)
+    return weights

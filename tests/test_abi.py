@@ -28,14 +28,15 @@ def test_header_declares_the_api():
     assert {"qs_abi_version", "qs_row_bytes", "qs_quantize", "qs_last_error",
             "qs_type_supported", "qs_type_needs_imatrix", "qs_type_uses_imatrix",
             "qs_device_count", "qs_pipeline_create", "qs_pipeline_quantize", "qs_pipeline_write",
-            "qs_pipeline_finish", "qs_pipeline_destroy"} <= names
+            "qs_pipeline_finish", "qs_pipeline_destroy", "qs_init", "qs_set_sqrt_rounding",
+            "qs_get_sqrt_rounding"} <= names
 
 
 def test_library_exports_every_declared_symbol(qs):
     L = qs.library()
     for name in declared_functions():
         assert hasattr(L, name), f"libqs_hip.so does not export {name}"
-    assert L.qs_abi_version() == qs.ABI_VERSION == 2
+    assert L.qs_abi_version() == qs.ABI_VERSION == 3
 
 
 @pytest.mark.parametrize("qtype", sorted(TYPES))
@@ -98,11 +99,17 @@ def test_needs_imatrix_types_reject_missing_imatrix(qs):
             assert b"requires an imatrix" in L.qs_last_error()
 
 
-def test_quant_fn_refuses_cpu_tensors(qs):
+def test_cpu_quant_fn_needs_a_rocm_device(qs):
+    """A quant_fn for a CPU device stages its tensors through the ROCm device;
+    with none present it fails loudly (there is no CPU arithmetic to fall back
+    on). The staged path itself is a GPU test."""
     import torch
-    fn = qs.QUANT_TYPES["q4_k"].make_kernel(torch.device("cpu"), None)
-    with pytest.raises(ValueError, match="ROCm device"):
-        fn(torch.zeros(2, 256))
+    if torch.cuda.is_available():
+        pytest.skip("a ROCm device is present: covered by the GPU tests")
+    for qw in (None, torch.ones(256)):
+        fn = qs.QUANT_TYPES["q4_k"].make_kernel(torch.device("cpu"), qw)
+        with pytest.raises(qs.QuantSpecError, match="no ROCm device"):
+            fn(torch.zeros(2, 256))
 
 
 def test_pipeline_rejects_bad_arguments_without_device_work(qs):
@@ -133,3 +140,26 @@ def test_one_hip_runtime_in_any_import_order():
                        timeout=300)
     assert r.returncode == 0, r.stderr
     assert r.stdout.strip() == "1"
+
+
+def test_sqrt_rounding_modes(qs):
+    """The process-wide square-root mode: torch-cpu by default, ieee on
+    request, anything else refused without changing the mode."""
+    L = qs.library()
+    assert qs.sqrt_rounding() == "torch-cpu"
+    try:
+        qs.set_sqrt_rounding("ieee")
+        assert L.qs_get_sqrt_rounding() == 1 and qs.sqrt_rounding() == "ieee"
+        assert L.qs_set_sqrt_rounding(7) == -22 and "square-root mode 7" in qs.last_error()
+        assert qs.sqrt_rounding() == "ieee"
+        with pytest.raises(ValueError):
+            qs.set_sqrt_rounding("fast")
+    finally:
+        qs.set_sqrt_rounding("torch-cpu")
+    assert L.qs_get_sqrt_rounding() == 0
+
+
+def test_init_refuses_absent_devices(qs):
+    L = qs.library()
+    assert L.qs_init(-1) == -22
+    assert L.qs_init(1 << 20) == -22 and "not present" in qs.last_error()

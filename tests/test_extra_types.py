@@ -257,3 +257,81 @@ def test_gpu_row_stride_chunking_and_unaligned_output(qs, dev, qtype):
     assert b[0] == 0 and b[-2:].tolist() == [0, 0]
     assert np.array_equal(b[1:1 + 40 * rb].reshape(40, rb), ref)
     assert np.array_equal(parts.cpu().numpy(), ref)
+
+
+# ------------------------------------------- ulp-level pin: a second restatement
+
+def _pin_inputs() -> np.ndarray:
+    """131,072 blocks of 32: normal, uniform, heavy-tailed and bf16-rounded
+    values at scales 1e-30 .. 1e4; exact half-way values of every format's
+    rounding; zero, constant, one-signed, subnormal and tied-absmax blocks."""
+    rng = np.random.default_rng(11)
+    n = 1 << 17
+    scale = np.exp(rng.uniform(np.log(1e-30), np.log(1e4), (n, 1)))
+    kind = rng.integers(0, 4, (n, 1))
+    v = np.where(kind == 0, rng.standard_normal((n, 32)),
+                 np.where(kind == 1, rng.uniform(-1, 1, (n, 32)),
+                          np.where(kind == 2, rng.standard_t(3, (n, 32)),
+                                   rng.standard_normal((n, 32)) + 3.0)))
+    x = (v * scale).astype(np.float32)
+    bf = rng.random(n) < 0.5                                  # half of them bf16 values
+    x[bf] = (x[bf].view(np.uint32) & np.uint32(0xffff0000)).view(np.float32)
+    # half-way cases: d = 1 (Q8_0 absmax 127; Q4_1/Q5_1 range nmax), values at k + 1/2
+    half = (rng.integers(-126, 126, (512, 32)) + 0.5).astype(np.float32)
+    half[:, 0] = 127.0
+    x[:512] = half
+    r15 = (rng.integers(0, 15, (512, 32)) + 0.5).astype(np.float32)
+    r15[:, 0], r15[:, 1] = 0.0, 15.0
+    x[512:1024] = r15
+    # Q5_0: d = -absmax/16 = 1 when the absmax is -16: x = k - 16.5 + ... lands on .5 after +16.5
+    r16 = (rng.integers(-15, 15, (512, 32)) + 0.5).astype(np.float32)
+    r16[:, 3] = -16.0
+    x[1024:1536] = r16
+    x[1536] = 0.0
+    x[1537] = 0.37
+    x[1538] = -0.0
+    x[1539] = np.abs(x[1539])
+    x[1540] = rng.integers(1, 1 << 23, 32).astype(np.uint32).view(np.float32)   # subnormals
+    x[1541, :] = 1.0
+    x[1541, 7] = -1.0                                         # tied |absmax|: first index wins
+    return x
+
+
+@pytest.mark.parametrize("qtype,imat", [("q4_1", False), ("q5_0", False), ("q5_1", False),
+                                        ("q8_0", False), ("iq4_nl", False), ("iq4_nl", True)])
+def test_oracle_matches_numpy_restatement_bit_for_bit(qtype, imat):
+    """The oracle against an independent numpy restatement of the same
+    formats, byte for byte on 131,072 blocks (the square root of IQ4_NL's
+    weights taken as IEEE by both)."""
+    import extra_types_np
+    x = _pin_inputs().reshape(-1, 256)
+    qw = np.random.default_rng(3).lognormal(0, 1, 256).astype(np.float32) if imat else None
+    want = extra_types_np.quantize(qtype, x, qw)
+    oracle.use_ieee_sqrt(True)
+    try:
+        got = quant(qtype, x, qw)
+    finally:
+        oracle.use_ieee_sqrt(False)
+    diff = ~(blocks(got, qtype) == blocks(want, qtype)).all(1)
+    assert not diff.any(), f"{int(diff.sum())} of {diff.size} blocks differ (first {np.nonzero(diff)[0][:5]})"
+
+
+# planted division slips in the oracle and the types whose pin must catch them
+DIVISION_SLIPS = {7: ("d = a * (1/n) instead of a / n", ["q4_1", "q5_1", "q8_0"]),
+                  8: ("x / d instead of x * (1/d)", ["q4_1", "q5_0", "q5_1", "q8_0", "iq4_nl"])}
+
+
+@pytest.mark.parametrize("mut", sorted(DIVISION_SLIPS))
+def test_numpy_pin_catches_division_slips(mut):
+    import extra_types_np
+    what, types = DIVISION_SLIPS[mut]
+    x = _pin_inputs().reshape(-1, 256)    # IQ4_NL's reprojection shows slip 8 in 1 block of them
+    L = oracle.lib()
+    L.qso_set_mutation(mut)
+    try:
+        for qtype in types:
+            got = quant(qtype, x)
+            want = extra_types_np.quantize(qtype, x)
+            assert not np.array_equal(got, want), f"slip '{what}' not caught for {qtype}"
+    finally:
+        L.qso_set_mutation(0)

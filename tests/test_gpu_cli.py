@@ -87,6 +87,44 @@ def test_schemes_with_imatrix(tmp_path, scheme, ftype, extra):
     check_output(src, out, expect, ftype=ftype, imatrix=imat)
 
 
+def test_device_cpu_writes_the_same_file(tmp_path):
+    """--device cpu (the reference's CPU path) and the default device give the
+    same file, byte for byte."""
+    src = tmp_path / "in.gguf"
+    expect = small_model(src, odd=False)
+    im = tmp_path / "im.gguf"
+    imatrix_for(im, {n: v.shape[-1] for n, v in expect.items()},
+                n_mat={"blk.0.ffn_gate_exps.weight": 4})
+    a, b = tmp_path / "a.gguf", tmp_path / "b.gguf"
+    run_cli(src, a, "Q4_K_M", "--imatrix", im)
+    r = run_cli(src, b, "Q4_K_M", "--imatrix", im, "--device", "cpu")
+    assert "device=cpu (on rocm)" in r.stdout
+    assert a.read_bytes() == b.read_bytes()
+
+
+@pytest.mark.parametrize("mode", ["torch-cpu-amd", "ieee"])
+def test_sqrt_rounding_option(tmp_path, mode):
+    """--sqrt-rounding reaches the kernels: every quantized tensor equals the
+    oracle in the same square-root mode."""
+    import sqrt_hosts
+    src = tmp_path / "in.gguf"
+    expect = small_model(src, odd=False)
+    im = tmp_path / "im.gguf"
+    imatrix_for(im, {n: v.shape[-1] for n, v in expect.items()},
+                n_mat={"blk.0.ffn_gate_exps.weight": 4})
+    out = tmp_path / "o.gguf"
+    run_cli(src, out, "IQ4_XS", "--imatrix", im, "--sqrt-rounding", mode)
+    if mode == "ieee":
+        oracle.use_ieee_sqrt(True)
+    else:
+        oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+    try:
+        check_output(src, out, expect, ftype=30, imatrix=io.load_imatrix(im))
+    finally:
+        oracle.use_ieee_sqrt(False)
+        oracle.use_sqrt_table(None)
+
+
 def test_pipeline_chunks_match_single_call_and_report_write_errors(tmp_path):
     """The native pipeline directly: any chunking writes the same bytes as one
     qs_quantize call (checked against the oracle), and a failing write (here a

@@ -198,3 +198,91 @@ def test_python_mirror_splits_calls_over_the_value_limit(dev, monkeypatch):
         monkeypatch.undo()
         assert np.array_equal(whole, split), qtype
         assert np.array_equal(whole, oracle.quantize(qtype, x, qw, n_threads=NTHREADS)), qtype
+
+
+# every type whose weights take a square root: the imatrix variants, plus
+# Q4_K / Q5_K without one (av_x = sqrt(sum x^2 / 32), q4_k.py:34)
+SQRT_CASES = [(t, True) for t in HIP_TYPES + ["iq4_nl"] if t != "q4_0"] + [("q4_k", False), ("q5_k", False)]
+
+
+@pytest.mark.parametrize("mode", ["ieee", "torch-cpu-amd"])
+@pytest.mark.parametrize("qtype,imat", SQRT_CASES)
+def test_sqrt_rounding_modes(qs, dev, mode, qtype, imat):
+    """The other square-root modes against the oracle in the same mode: the
+    IEEE root, and torch.sqrt as an AMD EPYC host's MKL rounds it (the map the
+    library embeds, decoded independently by the test)."""
+    import sqrt_hosts
+    x, qw = c2_like(192, 2560, seed=77 + sum(map(ord, qtype)))
+    qw = qw if imat else None
+    print(f"{qtype} imat={imat} sqrt={mode}", flush=True)
+    if mode == "ieee":
+        oracle.use_ieee_sqrt(True)
+    else:
+        oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+    try:
+        qs.set_sqrt_rounding(mode)
+        tid = int(qs.ALL_SPECS[qtype].ggml_type)
+        got = qs.quantize(tid, to_device(x, dev), None if qw is None else torch.from_numpy(qw).to(dev))
+        got = got.cpu().numpy()
+        ref = oracle.quantize(qtype, x, qw, n_threads=NTHREADS)
+    finally:
+        qs.set_sqrt_rounding("torch-cpu")
+        oracle.use_ieee_sqrt(False)
+        oracle.use_sqrt_table(None)
+    assert np.array_equal(got, ref), f"{qtype} sqrt={mode}: differs from the oracle"
+    # and the default mode is back: the golden-host bytes again
+    if imat:
+        back = qs.quantize(tid, to_device(x[:8], dev), torch.from_numpy(qw).to(dev)).cpu().numpy()
+        assert np.array_equal(back, oracle.quantize(qtype, x[:8], qw, n_threads=NTHREADS))
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q4_k", "iq2_xs", "iq3_s"])
+def test_cpu_device_quant_fn(qs, dev, qtype):
+    """make_kernel(cpu, qw) returns a quant_fn that takes CPU tensors and
+    returns a CPU uint8 tensor with the oracle's bytes (the reference's CPU
+    path, quant-studio.py:216-232), computing on the ROCm device."""
+    x, qw = c2_like(33, 512, seed=5)
+    spec = qs.QUANT_TYPES[qtype]
+    fn = spec.make_kernel(torch.device("cpu"), torch.from_numpy(qw))
+    xt = torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16)
+    got = fn(xt)
+    assert got.device.type == "cpu" and got.dtype == torch.uint8
+    ref = oracle.quantize(qtype, x, qw if spec.uses_imatrix else None, n_threads=NTHREADS)
+    assert np.array_equal(got.numpy(), ref)
+    # f32 CPU input, and the module-level call with a CPU tensor
+    got32 = qs.quantize(int(spec.ggml_type), xt.float(), torch.from_numpy(qw) if spec.uses_imatrix else None)
+    assert got32.device.type == "cpu" and np.array_equal(got32.numpy(), ref)
+
+
+def test_layouts_the_c_call_refuses_are_copied(qs, dev):
+    """Views the C call does not take (column offset not 16-byte aligned, row
+    stride not a multiple of 16 bytes, an expanded row) are quantized from a
+    contiguous copy: same bytes as the contiguous tensor."""
+    x, qw = c2_like(24, 512, seed=8)
+    base = torch.zeros((24, 512 + 40), dtype=torch.bfloat16, device=dev)
+    base[:, 1:513] = to_device(x, dev)
+    odd = torch.zeros((24, 516), dtype=torch.bfloat16, device=dev)
+    odd[:, :512] = to_device(x, dev)
+    q = torch.from_numpy(qw).to(dev)
+    views = {"column offset 1 (2 bytes)": base[:, 1:513],
+             "row stride 1032 bytes": odd[:, :512]}
+    for qtype in ("q4_0", "q4_k", "iq3_xxs"):
+        tid = TYPES[qtype][0]
+        ref = oracle.quantize(qtype, x, None if qtype == "q4_0" else qw, n_threads=NTHREADS)
+        for name, v in views.items():
+            assert np.array_equal(qs.quantize(tid, v, q).cpu().numpy(), ref), (qtype, name)
+        row = to_device(x[:1], dev).expand(5, 512)
+        assert row.stride(0) == 0
+        got = qs.quantize(tid, row, q).cpu().numpy()
+        assert np.array_equal(got, np.repeat(ref[:1], 5, axis=0)), (qtype, "expanded")
+
+
+def test_init_uploads_tables_up_front(qs, dev):
+    """qs_init on the device succeeds (again, too), and quantization then
+    behaves as before on every table it uploaded."""
+    qs.init(0)
+    qs.init(0)
+    x, qw = c2_like(16, 512, seed=6)
+    for qtype in ("q4_k", "iq2_s", "iq3_s"):
+        assert np.array_equal(hip_quantize(qs, qtype, x, qw, dev),
+                              oracle.quantize(qtype, x, qw, n_threads=NTHREADS))
