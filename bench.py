@@ -620,7 +620,7 @@ def main() -> int:
         elif args.sqrt == "torch-cpu-amd":
             sys.path.insert(0, str(ROOT / "tests"))
             import sqrt_hosts
-            oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+            oracle.use_amd_host_sqrt(sqrt_hosts.amd_ulps())
         cb = cpu_baseline(oracle, host, qws, gpu_out, args.cpu_seconds)
         line["cpu_baseline"] = cb
         head = cb["per_type"].get("q4_k+imat")

@@ -59,7 +59,7 @@ def lib() -> ctypes.CDLL:
         L.qso_set_sqrt_ieee.restype = None
         L.qso_set_sqrt_ieee.argtypes = [ctypes.c_int]
         L.qso_set_sqrt_table.restype = None
-        L.qso_set_sqrt_table.argtypes = [ctypes.c_void_p]
+        L.qso_set_sqrt_table.argtypes = [ctypes.c_void_p, ctypes.c_int]
         L.qso_sqrt.restype = ctypes.c_float
         L.qso_sqrt.argtypes = [ctypes.c_float]
         L.qso_sqrt_ref.restype = ctypes.c_float
@@ -117,20 +117,27 @@ def use_ieee_sqrt(enable: bool) -> None:
 _sqrt_table = None
 
 
-def use_sqrt_table(ulps) -> None:
+def use_sqrt_table(ulps, subnormal_ieee: bool = False) -> None:
     """Make the oracle round its square roots by a per-key table: `ulps` holds
     2^24 int8 offsets from the IEEE root (torch.sqrt measured on another host),
-    keyed like qso_sqrt_ref; None switches the table off (tests only)."""
+    keyed like qso_sqrt_ref; with subnormal_ieee, subnormal inputs keep the IEEE
+    root; None switches the table off (tests only)."""
     global _sqrt_table
     if ulps is None:
-        lib().qso_set_sqrt_table(None)
+        lib().qso_set_sqrt_table(None, 0)
         _sqrt_table = None
         return
     t = np.ascontiguousarray(ulps, dtype=np.int8)
     if t.size != 1 << 24:
         raise ValueError("the square-root table holds one offset per 2^24 keys")
-    lib().qso_set_sqrt_table(t.ctypes.data)
+    lib().qso_set_sqrt_table(t.ctypes.data, 1 if subnormal_ieee else 0)
     _sqrt_table = t
+
+
+def use_amd_host_sqrt(ulps) -> None:
+    """The AMD EPYC host's torch.sqrt: the table `ulps` on normal inputs, the
+    IEEE root on subnormal ones (tests only; None switches it off)."""
+    use_sqrt_table(ulps, subnormal_ieee=True)
 
 
 def use_torch_sqrt(enable: bool) -> None:

@@ -87,14 +87,20 @@ float qso_sqrt_ref(float v) {
 
 /* Another host's torch.sqrt rounding, given as a per-key offset in ulps from
  * the IEEE root (2^24 int8 entries, same keys as above): the rounding measured
- * on a host whose MKL takes a different code path (tests only). */
+ * on a host whose MKL takes a different code path (tests only). With
+ * subnormal_ieee set, subnormal inputs keep the IEEE root (the AMD EPYC host's
+ * torch.sqrt does on all 2^23 - 1 of them). */
 static const int8_t *g_sqrt_ulps = 0;
-void qso_set_sqrt_table(const int8_t *ulps) { g_sqrt_ulps = ulps; }
+static int g_sqrt_sub_ieee = 0;
+void qso_set_sqrt_table(const int8_t *ulps, int subnormal_ieee) {
+    g_sqrt_ulps = ulps;
+    g_sqrt_sub_ieee = subnormal_ieee;
+}
 static float sqrt_table_ulps(float v) {
     float r = sqrtf(v);
     uint32_t b;
     memcpy(&b, &v, 4);
-    if (b - 1u < 0x7f7fffffu) {
+    if (b - 1u < 0x7f7fffffu && !(g_sqrt_sub_ieee && b < 0x00800000u)) {
         if (b < 0x00800000u) {
             float n = v * 18446744073709551616.0f;
             memcpy(&b, &n, 4);

@@ -52,7 +52,7 @@ void qso_set_sqrt_ieee(int on);
 /* Test hook: a per-key rounding table (2^24 int8 ulp offsets from the IEEE
  * root, keyed as qso_sqrt_ref; NULL = off), e.g. torch.sqrt measured on
  * another host. The caller keeps the table alive while it is installed. */
-void qso_set_sqrt_table(const int8_t *ulps);
+void qso_set_sqrt_table(const int8_t *ulps, int subnormal_ieee);
 /* The square root the weights currently use (whichever of the above is set). */
 float qso_sqrt(float v);
 /* Neighbour list of an off-grid code (tables 0..4: IQ2 256/512/1024, IQ3 256/512):

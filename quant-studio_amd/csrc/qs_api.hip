@@ -23,6 +23,7 @@
 #include "qs_host.h"
 #include "qs_iq.h"
 #include "qs_kernels.h"
+#include "qs_launch.h"
 #include "qs_sqrt_table.h"
 
 namespace {
@@ -113,7 +114,7 @@ bool has_kernel(int id) { return find_type(id) != nullptr; }
 
 // ---- IQ grid tables: built once per process, uploaded once per device ----
 
-enum IqTabId { IQT_G2_256, IQT_G2_512, IQT_G2_1024, IQT_G3_256, IQT_G3_512, IQT_N };
+using namespace qs_launch;      // IqTabId, launch_src
 
 struct HostTab {
     std::vector<uint16_t> grid, nbr;
@@ -213,11 +214,6 @@ std::mutex g_dev_mutex;
 // rounded one ulp down and one ulp up (qs_sqrt_amd.bin).
 enum SqrtMapId { SQM_INTEL_DOWN, SQM_AMD_DOWN, SQM_AMD_UP, SQM_N };
 
-// lookup bands of the two hosts' maps, in units of r * ulp(r) (qs::SqrtMap;
-// both proven over all 2^24 keys by the tests)
-constexpr float kIntelBandLo = -0.875f;
-constexpr float kAmdBand = 0.48f;
-
 // Per-device constant tables: the IQ grids and neighbour lists, and the
 // square-root maps.
 struct DevTables {
@@ -308,150 +304,15 @@ bool device_tables(int iq_table, int sqrt_mode, DevTables& out) {
     return device_tables_locked(dev, iq_table, maps_of(sqrt_mode), out);
 }
 
-// the kernels' view of a square-root mode
+// the kernels' view of a square-root mode: the maps, and the template kind
 qs::SqrtMap sqrt_map(int mode, const DevTables& t) {
-    qs::SqrtMap m{};
-    const float inf = __builtin_inff();
-    if (mode == QS_SQRT_TORCH_CPU) m = {t.sqrt[SQM_INTEL_DOWN], nullptr, kIntelBandLo, inf};
-    else if (mode == QS_SQRT_TORCH_CPU_AMD) m = {t.sqrt[SQM_AMD_DOWN], t.sqrt[SQM_AMD_UP], -kAmdBand, kAmdBand};
-    else m = {nullptr, nullptr, 0.0f, 0.0f};      // QS_SQRT_IEEE
-    return m;
+    if (mode == QS_SQRT_TORCH_CPU) return {t.sqrt[SQM_INTEL_DOWN], nullptr};
+    if (mode == QS_SQRT_TORCH_CPU_AMD) return {t.sqrt[SQM_AMD_DOWN], t.sqrt[SQM_AMD_UP]};
+    return {nullptr, nullptr};      // QS_SQRT_IEEE
 }
 
-// Launch through hipLaunchKernel so its status comes back as the return
-// value: the caller's pending hipGetLastError() state is neither read nor
-// reset by this library.
-template <typename... P, typename... A>
-hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t st, A&&... args) {
-    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
-    std::tuple<P...> vals(std::forward<A>(args)...);
-    void* argv[sizeof...(P)];
-    std::apply([&](auto&... v) {
-        int i = 0;
-        ((argv[i++] = static_cast<void*>(&v)), ...);
-    }, vals);
-    return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, argv, 0, st);
-}
-
-qs::IqSteps iq_steps(float base, float delta, int lo, int hi) {
-    qs::IqSteps s{};
-    s.n = 0;
-    for (int i = lo; i <= hi; i++) {
-        float t = (float)i * delta;
-        s.v[s.n++] = base + t;
-    }
-    return s;
-}
-
-// candidate numerators, f32 chains as kq_common.py:21-30 and qx_common.py:20-23
-qs::Steps qkx_steps(float rmin, float rdelta, int nstep, int nmax) {
-    qs::Steps s{};
-    for (int i = 0; i <= nstep; i++) {
-        float t = rdelta * (float)i;
-        t = rmin + t;
-        s.v[i] = t + (float)nmax;
-    }
-    s.n = nstep + 1;
-    return s;
-}
-
-qs::QpSteps qp_steps(int nmax) {
-    qs::QpSteps s{};
-    int n = 0;
-    for (int i = -4; i <= 4; i++) {
-        if (!i) continue;
-        float t = 0.1f * (float)i;
-        s.v[n++] = t + (float)nmax;
-    }
-    return s;
-}
-
-qs::Steps qx_steps(int nmax) {
-    qs::Steps s{};
-    int n = 0;
-    for (int i = -9; i <= 9; i++) {
-        if (!i) continue;
-        float t = 0.1f * (float)i;
-        s.v[n++] = (float)nmax + t;
-    }
-    s.n = n;
-    return s;
-}
-
-template <int SRC, qs::B32 T>
-hipError_t launch_b32(const qs::KArgs& a, hipStream_t st) {
-    const unsigned g = (unsigned)((a.n_units + qs::Q40_BLOCKS_PER_WG - 1) / qs::Q40_BLOCKS_PER_WG);
-    return launch(qs::k_b32<SRC, T>, dim3(g), dim3(256), st, a);
-}
-
-template <int SRC>
-hipError_t launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
-                       const std::array<qs::IqTabDev, IQT_N>& tabs) {
-    using namespace qs;
-    const dim3 wave(64);
-    const dim3 sb8((unsigned)((a.n_units + 7) / 8)), sb4((unsigned)((a.n_units + 3) / 4));
-    switch (type) {
-    case QS_TYPE_Q4_0: return launch_b32<SRC, B32::Q4_0>(a, st);
-    case QS_TYPE_Q4_1: return launch_b32<SRC, B32::Q4_1>(a, st);
-    case QS_TYPE_Q5_0: return launch_b32<SRC, B32::Q5_0>(a, st);
-    case QS_TYPE_Q5_1: return launch_b32<SRC, B32::Q5_1>(a, st);
-    case QS_TYPE_Q8_0: return launch_b32<SRC, B32::Q8_0>(a, st);
-    case QS_TYPE_IQ4_NL: {
-        const dim3 g((unsigned)((a.n_units + 63) / 64));
-        return imat ? launch(k_iq4_nl<SRC, true>, g, wave, st, a)
-                    : launch(k_iq4_nl<SRC, false>, g, wave, st, a);
-    }
-    case QS_TYPE_Q4_K:
-        return imat ? launch(k_q45_k<SRC, true, 15>, sb8, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 15),
-                             qp_steps(63))
-                    : launch(k_q45_k<SRC, false, 15>, sb8, wave, st, a, qkx_steps(-1.0f, 0.1f, 20, 15),
-                             qp_steps(63));
-    case QS_TYPE_Q5_K:
-        return imat ? launch(k_q45_k<SRC, true, 31>, sb8, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 31),
-                             qp_steps(63))
-                    : launch(k_q45_k<SRC, false, 31>, sb8, wave, st, a, qkx_steps(-0.5f, 0.1f, 15, 31),
-                             qp_steps(63));
-    case QS_TYPE_Q6_K:
-        return imat ? launch(k_q6_k<SRC, true>, sb4, wave, st, a, qx_steps(32))
-                    : launch(k_q6_k<SRC, false>, sb4, wave, st, a, qx_steps(32));
-    case QS_TYPE_Q3_K:
-        return imat ? launch(k_q3_k<SRC, true>, sb4, wave, st, a, qx_steps(4), qx_steps(32))
-                    : launch(k_q3_k<SRC, false>, sb4, wave, st, a, qx_steps(4), qx_steps(32));
-    case QS_TYPE_Q2_K:
-        return imat ? launch(k_q2_k<SRC, true>, sb4, wave, st, a, qkx_steps(-0.9f, 0.05f, 36, 3),
-                             qp_steps(15))
-                    : launch(k_q2_k<SRC, false>, sb4, wave, st, a, qkx_steps(-0.5f, 0.1f, 15, 3),
-                             qp_steps(15));
-    case QS_TYPE_IQ4_XS:
-        return imat ? launch(k_iq4_xs<SRC, true>, sb8, wave, st, a)
-                    : launch(k_iq4_xs<SRC, false>, sb8, wave, st, a);
-    case QS_TYPE_IQ2_XXS: {
-        // candidate numerators computed in f64 and rounded once (iq2.py:387, :470)
-        QpSteps qp4{};
-        IqSteps sweep{};
-        int n = 0;
-        for (int i = -4; i <= 4; i++)
-            if (i) qp4.v[n++] = (float)(0.1 * i + 4.0);
-        for (int i = -6; i <= 6; i++) sweep.v[sweep.n++] = (float)(5.0 + 0.1 * i);
-        return launch(k_iq2_xxs<SRC>, sb8, wave, st, a, tabs[IQT_G2_256], qp4, sweep);
-    }
-    case QS_TYPE_IQ2_XS:      // SWEEP_CS iq2xs_common.py:21
-        return launch(k_iq2_xs_s<SRC, false>, sb4, wave, st, a, tabs[IQT_G2_512],
-                      iq_steps(5.0f, 0.1f, -9, 9));
-    case QS_TYPE_IQ2_S:
-        return launch(k_iq2_xs_s<SRC, true>, sb4, wave, st, a, tabs[IQT_G2_1024],
-                      iq_steps(5.0f, 0.1f, -9, 9));
-    case QS_TYPE_IQ3_XXS:     // _STEPS iq3_xxs.py:22
-        return launch(k_iq3<SRC, false, true>, sb8, wave, st, a, tabs[IQT_G3_256],
-                      iq_steps(15.0f, 0.2f, -15, 15));
-    case QS_TYPE_IQ3_S:       // _STEPS iq3_s.py:22
-        return imat ? launch(k_iq3<SRC, true, true>, sb8, wave, st, a, tabs[IQT_G3_512],
-                             iq_steps(15.0f, 0.2f, -9, 9))
-                    : launch(k_iq3<SRC, true, false>, sb8, wave, st, a, tabs[IQT_G3_512],
-                             iq_steps(15.0f, 0.2f, -9, 9));
-    default:
-        return hipErrorInvalidValue;
-    }
+int sqrt_kind(int mode) {
+    return mode == QS_SQRT_TORCH_CPU ? qs::SQ_INTEL : mode == QS_SQRT_TORCH_CPU_AMD ? qs::SQ_AMD : qs::SQ_IEEE;
 }
 
 }  // namespace
@@ -536,9 +397,9 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     a.sqrt = sqrt_map(mode, tabs);
     hipError_t e;
     switch (src_type) {
-    case QS_SRC_F32: e = launch_type<qs::SRC_F32>(ggml_type, imat, a, st, tabs.iq); break;
-    case QS_SRC_F16: e = launch_type<qs::SRC_F16>(ggml_type, imat, a, st, tabs.iq); break;
-    default: e = launch_type<qs::SRC_BF16>(ggml_type, imat, a, st, tabs.iq); break;
+    case QS_SRC_F32: e = launch_src<qs::SRC_F32>(sqrt_kind(mode), ggml_type, imat, a, st, tabs.iq); break;
+    case QS_SRC_F16: e = launch_src<qs::SRC_F16>(sqrt_kind(mode), ggml_type, imat, a, st, tabs.iq); break;
+    default: e = launch_src<qs::SRC_BF16>(sqrt_kind(mode), ggml_type, imat, a, st, tabs.iq); break;
     }
     if (e != hipSuccess) return fail(QS_EIO, "%s: launch failed: %s", t->name, hipGetErrorString(e));
     return 0;

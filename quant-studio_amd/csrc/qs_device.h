@@ -10,8 +10,8 @@
 //     (two roundings), which rdiv() restates;
 //   - torch.round is round-half-even: rintf -> v_rndne_f32;
 //   - torch.sqrt on a CPU tensor is not correctly rounded, and how it rounds
-//     depends on the host's MKL: sqrt_ref() is the IEEE root adjusted by one
-//     ulp on the tabulated keys of the selected host (or left IEEE).
+//     depends on the host's MKL: sqrt_ref<SQ>() is the IEEE root adjusted by
+//     one ulp on the tabulated keys of the selected host (or left IEEE).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -56,24 +56,40 @@ QS_DEV void keep_in_registers(float (&v)[N]) {
 
 // The reference's square root (torch.sqrt, kernels/q4_k.py:34, :51,
 // iq2.py:431, :436 and the other weight sites), whose rounding depends on the
-// host it ran on. SqrtMap selects it:
-//   down == nullptr: the IEEE root (torch.sqrt on a GPU tensor, C sqrtf);
-//   else the IEEE root, one ulp lower where the input's key is set in `down`
-//   and one ulp higher where it is set in `up` (nullptr: never), with the key
-//   (exponent parity << 23 | mantissa, subnormals scaled by 2^64 first)
-//   indexing two 2^24-bit maps built per device from the measured tables.
-// The maps are read only where the exact root s can lie on the flipped side:
-// with r the IEEE root and rem = v - r^2 (exact, fma(-r, r, v)),
-// s - r = rem / (s + r), and every tabulated key has rem below band_lo * r *
-// ulp(r) (down) or above band_hi * r * ulp(r) (up), checked over all 2^24 keys
-// on the host; below 2^-80 the products lose precision and the map is always
-// read. Zero, negative, infinite and NaN inputs keep the IEEE result. Lanes
-// that need no lookup read word 0 (one shared cache line).
+// host it ran on. The kernels take the host as a template parameter SQ, so
+// each compiles only the lookups its rounding needs (a runtime choice kept a
+// second map's words live in every kernel and spilled the tightest ones):
+//   SQ_IEEE   the correctly rounded root (torch.sqrt on a GPU tensor, sqrtf);
+//   SQ_INTEL  torch.sqrt on an Intel host's CPU: the IEEE root, one ulp lower
+//             where the input's key is set in the `down` map; subnormal
+//             inputs follow the key of their value scaled by 2^64;
+//   SQ_AMD    torch.sqrt on an AMD EPYC host's CPU: one ulp lower where the
+//             key is set in `down`, one ulp higher where it is set in `up`;
+//             subnormal inputs keep the IEEE root (measured on all 2^23 - 1).
+// The key is (exponent parity << 23 | mantissa); the 2^24-bit maps are built
+// per device from the measured tables. BAND variants read the maps only where
+// the exact root s can lie on the flipped side: with r the IEEE root and
+// rem = v - r^2 (exact, fma(-r, r, v)), s - r = rem / (s + r), and every
+// tabulated key has rem below lo * r * ulp(r) (down) or above hi * r * ulp(r)
+// (up), with (lo, hi) = (-0.875, none) on the Intel host and (-0.48, 0.48) on
+// the AMD host, both checked over all 2^24 keys on the host; below 2^-80 the
+// products lose precision and the maps are always read. Zero, negative,
+// infinite and NaN inputs keep the IEEE result. Lanes that need no lookup
+// read word 0 (one shared cache line).
+enum : int { SQ_IEEE = 0, SQ_INTEL = 1, SQ_AMD = 2 };
+
 struct SqrtMap {
     const uint32_t* down;
     const uint32_t* up;
-    float band_lo, band_hi;
 };
+
+// true for inputs the maps apply to: positive finite (Intel), positive
+// normal finite (AMD)
+template <int SQ>
+QS_DEV bool sqrt_mapped(uint32_t b) {
+    constexpr uint32_t lo = SQ == SQ_AMD ? 0x00800000u : 1u;
+    return b - lo < 0x7f800000u - lo;
+}
 
 QS_DEV uint32_t sqrt_key(float v) {
     const uint32_t b = __float_as_uint(v);
@@ -82,20 +98,33 @@ QS_DEV uint32_t sqrt_key(float v) {
 }
 
 // The map key with bit 31 set when the maps must be read for v (root r), else 0.
-QS_DEV uint32_t sqrt_lookup_key(float v, float r, const SqrtMap& m) {
+template <int SQ>
+QS_DEV uint32_t sqrt_lookup_key(float v, float r) {
     const float rem = __builtin_fmaf(-r, r, v);
     const float ulp = __uint_as_float((__float_as_uint(r) & 0x7f800000u) - (23u << 23));
-    const float lim_lo = (m.band_lo * r) * ulp, lim_hi = (m.band_hi * r) * ulp;
     const uint32_t b = __float_as_uint(v);
-    const bool look = (b - 1u < 0x7f7fffffu) && (rem < lim_lo || rem > lim_hi || b < 0x17800000u);
+    bool outside;
+    if constexpr (SQ == SQ_AMD) {
+        const float lim = (0.48f * r) * ulp;
+        outside = rem < -lim || rem > lim;
+    } else {
+        outside = rem < (-0.875f * r) * ulp;
+    }
+    const bool look = sqrt_mapped<SQ>(b) && (outside || b < 0x17800000u);
     return look ? (sqrt_key(v) | 0x80000000u) : 0u;
 }
 
 // r adjusted by the looked-up map bits (kn from sqrt_lookup_key)
+template <int SQ>
 QS_DEV float sqrt_fix(float r, uint32_t kn, uint32_t wdown, uint32_t wup) {
     const uint32_t sh = kn & 31u, on = kn >> 31;
-    const uint32_t dn = on & (wdown >> sh), up = on & (wup >> sh);
-    return __uint_as_float(__float_as_uint(r) - (dn & 1u) + (up & 1u));
+    const uint32_t dn = on & (wdown >> sh);
+    if constexpr (SQ == SQ_AMD) {
+        const uint32_t up = on & (wup >> sh);
+        return __uint_as_float(__float_as_uint(r) - (dn & 1u) + (up & 1u));
+    } else {
+        return __uint_as_float(__float_as_uint(r) - (dn & 1u));
+    }
 }
 
 QS_DEV uint32_t sqrt_word(const uint32_t* __restrict__ map, uint32_t kn) {
@@ -103,70 +132,69 @@ QS_DEV uint32_t sqrt_word(const uint32_t* __restrict__ map, uint32_t kn) {
 }
 
 // r = sqrtf(v) adjusted by the key's bits when every input reads its own words
+template <int SQ>
 QS_DEV float sqrt_fix_plain(float v, uint32_t key, uint32_t wdown, uint32_t wup) {
     const float r = sqrtf(v);
-    const uint32_t on = (__float_as_uint(v) - 1u < 0x7f7fffffu) ? 1u : 0u;
-    const uint32_t dn = on & (wdown >> (key & 31u)), up = on & (wup >> (key & 31u));
-    return __uint_as_float(__float_as_uint(r) - (dn & 1u) + (up & 1u));
+    const bool on = sqrt_mapped<SQ>(__float_as_uint(v));
+    const bool dn = on && ((wdown >> (key & 31u)) & 1u);
+    if constexpr (SQ == SQ_AMD) {
+        const bool up = on && ((wup >> (key & 31u)) & 1u);
+        return __uint_as_float(__float_as_uint(r) - (dn ? 1u : 0u) + (up ? 1u : 0u));
+    } else {
+        return dn ? __uint_as_float(__float_as_uint(r) - 1u) : r;
+    }
 }
 
-// The test on the map pointers is on kernel arguments, so every branch on
-// them is uniform.
+template <int SQ>
 QS_DEV float sqrt_ref(float v, const SqrtMap& m) {
-    if (!m.down) return sqrtf(v);
-    const uint32_t key = sqrt_key(v);
-    return sqrt_fix_plain(v, key, m.down[key >> 5], m.up ? m.up[key >> 5] : 0u);
+    if constexpr (SQ == SQ_IEEE) {
+        return sqrtf(v);
+    } else {
+        const uint32_t key = sqrt_key(v);
+        return sqrt_fix_plain<SQ>(v, key, m.down[key >> 5], SQ == SQ_AMD ? m.up[key >> 5] : 0u);
+    }
 }
 
 // sqrt_ref over a lane's N values, every map load issued before any is used.
 // BAND reads the maps only where sqrt_lookup_key asks; without it every value
 // reads its own words, which keeps fewer registers live: the Q4_K/Q5_K
 // kernels measured 1-2% faster that way, the others 2-17% slower.
-template <int N, bool BAND = true>
+template <int N, bool BAND, int SQ>
 QS_DEV void sqrt_ref_n(const float (&v)[N], const SqrtMap& m, float (&out)[N]) {
-    if (!m.down) {
+    if constexpr (SQ == SQ_IEEE) {
 #pragma unroll
         for (int i = 0; i < N; i++) out[i] = sqrtf(v[i]);
         return;
     }
+    constexpr bool UP = SQ == SQ_AMD;
     uint32_t kn[N], wd[N], wu[N];
     if constexpr (BAND) {
 #pragma unroll
         for (int i = 0; i < N; i++) {
             out[i] = sqrtf(v[i]);
-            kn[i] = sqrt_lookup_key(v[i], out[i], m);
+            kn[i] = sqrt_lookup_key<SQ>(v[i], out[i]);
         }
 #pragma unroll
         for (int i = 0; i < N; i++) wd[i] = sqrt_word(m.down, kn[i]);
-        if (m.up) {
 #pragma unroll
-            for (int i = 0; i < N; i++) wu[i] = sqrt_word(m.up, kn[i]);
-        } else {
+        for (int i = 0; i < N; i++) wu[i] = UP ? sqrt_word(m.up, kn[i]) : 0u;
 #pragma unroll
-            for (int i = 0; i < N; i++) wu[i] = 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < N; i++) out[i] = sqrt_fix(out[i], kn[i], wd[i], wu[i]);
+        for (int i = 0; i < N; i++) out[i] = sqrt_fix<SQ>(out[i], kn[i], wd[i], wu[i]);
     } else {
 #pragma unroll
         for (int i = 0; i < N; i++) kn[i] = sqrt_key(v[i]);
 #pragma unroll
         for (int i = 0; i < N; i++) wd[i] = m.down[kn[i] >> 5];
-        if (m.up) {
 #pragma unroll
-            for (int i = 0; i < N; i++) wu[i] = m.up[kn[i] >> 5];
-        } else {
+        for (int i = 0; i < N; i++) wu[i] = UP ? m.up[kn[i] >> 5] : 0u;
 #pragma unroll
-            for (int i = 0; i < N; i++) wu[i] = 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < N; i++) out[i] = sqrt_fix_plain(v[i], kn[i], wd[i], wu[i]);
+        for (int i = 0; i < N; i++) out[i] = sqrt_fix_plain<SQ>(v[i], kn[i], wd[i], wu[i]);
     }
 }
 
 // imatrix weights w[i] = qw[i] * sqrt_ref(sigma2 + x[i]^2) (e.g. q4_k.py:51),
 // with the imatrix and map loads issued together
-template <int N, bool BAND = true>
+template <int N, bool BAND, int SQ>
 QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const float (&x)[N],
                             const SqrtMap& m, float (&w)[N]) {
     float v[N], q[N];
@@ -177,7 +205,7 @@ QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const fl
         q[i] = qw[i];
     }
     float r[N];
-    sqrt_ref_n<N, BAND>(v, m, r);
+    sqrt_ref_n<N, BAND, SQ>(v, m, r);
 #pragma unroll
     for (int i = 0; i < N; i++) w[i] = q[i] * r[i];
 }

@@ -413,7 +413,7 @@ struct IqSteps {
     int n;
 };
 
-template <int SRC, int LPS, int GROUP>
+template <int SRC, int LPS, int GROUP, int SQ>
 QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K], float (*tmp)[40],
                             float sig_mult, bool use_x2, float (&x)[GROUP], float (&w)[GROUP]) {
     constexpr int SPW = 64 / LPS;
@@ -425,13 +425,13 @@ QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K],
     }
     const float sum = sb_sumsq_halves<LPS, SPW, GROUP>(vlds, tmp, x, p.slot, p.g);
     const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
-    imatrix_weights<GROUP>(a.qw + p.col, sigma2, x, a.sqrt, w);
+    imatrix_weights<GROUP, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
 }
 
 // ------------------------------------------------------------------
 // IQ2_XXS  quantize_iq2_xxs iq2.py:418-498 (+ _finalize :87-108)
 // ------------------------------------------------------------------
-template <int SRC>
+template <int SRC, int SQ>
 // 3 waves per SIMD (168 VGPRs, some spills): 9% faster than 2 waves unspilled
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq2_xxs(KArgs a, IqTabDev T, QpSteps qp4, IqSteps sweep) {
     constexpr int LPS = 8, SPW = 8, BYTES = 66;
@@ -443,8 +443,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
-    iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 1.0f, false, x, w);
-    sqrt_ref_n<32>(w, a.sqrt, waux);
+    iq_load_weights<SRC, LPS, 32, SQ>(a, p, s.v, s.tmp, 1.0f, false, x, w);
+    sqrt_ref_n<32, true, SQ>(w, a.sqrt, waux);
     keep_in_registers(waux);
     int signs[4];
     static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 // IQ2_XS / IQ2_S  scale_search iq2xs_common.py:280-342; quantize_iq2_xs
 // iq2_xs.py:20-69; quantize_iq2_s iq2_s.py:21-62
 // ------------------------------------------------------------------
-template <int SRC, bool IS_S>
+template <int SRC, bool IS_S, int SQ>
 // IQ2_XS fits 4 waves per SIMD in 128 VGPRs without spills (8% faster than
 // 3); IQ2_S is held to 3 by its LDS (the 1024-entry grid) and spills at 128
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4))) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
@@ -552,8 +552,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
     const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
-    iq_load_weights<SRC, LPS, 16>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
-    sqrt_ref_n<16>(w, a.sqrt, waux);
+    iq_load_weights<SRC, LPS, 16, SQ>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
+    sqrt_ref_n<16, true, SQ>(w, a.sqrt, waux);
     int signs[2];
     if constexpr (IS_S) {
         signs[0] = sign_bits8<0>(x, xval);
@@ -669,7 +669,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
 // IQ3_XXS / IQ3_S  quantize_iq3_xxs iq3_xxs.py:31-134, quantize_iq3_s
 // iq3_s.py:31-140
 // ------------------------------------------------------------------
-template <int SRC, bool IS_S, bool IMAT>
+template <int SRC, bool IS_S, bool IMAT, int SQ>
 // 3 waves per SIMD where it pays (IQ3_XXS 22%, IQ3_S without imatrix 12%
 // faster than 2); IQ3_S with imatrix spills too much at 3 and keeps 2
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT ? 2 : 3))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
@@ -684,8 +684,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT
     const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[32], w[32], waux[32], xval[32];
-    iq_load_weights<SRC, LPS, 32>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
-    sqrt_ref_n<32>(w, a.sqrt, waux);
+    iq_load_weights<SRC, LPS, 32, SQ>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
+    sqrt_ref_n<32, true, SQ>(w, a.sqrt, waux);
     keep_in_registers(waux);
     int signs[4];
     if constexpr (IS_S) {

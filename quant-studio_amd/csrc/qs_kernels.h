@@ -305,7 +305,8 @@ QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x
 // ------------------------------------------------------------------
 // Q4_K / Q5_K  (q4_k.py:25-79, q5_k.py:25-82)
 // ------------------------------------------------------------------
-template <int SRC, bool IMAT, int NMAX>
+template <int SRC, bool IMAT, int NMAX, int SQ>
+// SQ: the host whose square-root rounding the weights take (SQ_*).
 // Occupancy: the imatrix variant (143 VGPRs) runs 3 waves per SIMD; the other
 // (131) is held to 128 for a fourth wave: its 6 spilled registers cost one
 // scratch store on an accepted candidate and reloads after the candidate
@@ -328,12 +329,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4
         wave_sync();
         const float sum = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g);
         const float sigma2 = (2.0f * sum) / 256.0f;
-        imatrix_weights<32, false>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, false, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
         float t[32];
 #pragma unroll
         for (int i = 0; i < 32; i++) t[i] = x[i] * x[i];
-        const float av = sqrt_ref(cascade8_sum(t) / 32.0f, a.sqrt);
+        const float av = sqrt_ref<SQ>(cascade8_sum(t) / 32.0f, a.sqrt);
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = av + fabsf(x[i]);
     }
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(64) void k_q6_k(KArgs a, Steps steps) {
 // ------------------------------------------------------------------
 // Q3_K  (q3_k.py:23-78)
 // ------------------------------------------------------------------
-template <int SRC, bool IMAT>
+template <int SRC, bool IMAT, int SQ>
 __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps32) {
     constexpr int LPS = 16, SPW = 4, BYTES = 110;
     __shared__ SbLds<SPW, BYTES> s;
@@ -535,7 +536,7 @@ __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps3
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = (2.0f * sb_seq_256(s.v[slot])) / 256.0f;
-        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<16, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
         const QxResult r = qx_fit<16>(x, w, 4, steps4);
 #pragma unroll
         for (int i = 0; i < 16; i++) Lg[i] = qx_level(r, x[i], 4.0f);
@@ -606,7 +607,7 @@ __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps3
 // ------------------------------------------------------------------
 // Q2_K  (q2_k.py:25-81)
 // ------------------------------------------------------------------
-template <int SRC, bool IMAT>
+template <int SRC, bool IMAT, int SQ>
 __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) {
     constexpr int LPS = 16, SPW = 4, BYTES = 84;
     __shared__ SbLds<SPW, BYTES> s;
@@ -643,7 +644,7 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
         for (int i = 0; i < 16; i++) s.v[slot][16 * g + i] = x[i] * x[i];
         wave_sync();
         const float sigma2 = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g) / 256.0f;
-        imatrix_weights<16>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<16, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
         r = qkx_fit<16, false>(x, w, steps, 3.0f);
         s.sc[slot][g] = r.scale;
         s.mn[slot][g] = r.the_min;
@@ -715,7 +716,7 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
 // ------------------------------------------------------------------
 // IQ4_XS  (iq4_xs.py:149-188)
 // ------------------------------------------------------------------
-template <int SRC, bool IMAT>
+template <int SRC, bool IMAT, int SQ>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_xs(KArgs a) {
     constexpr int LPS = 8, SPW = 8, BYTES = 136;
     // LDS is what limits this kernel's residency: the imatrix path stages x^2
@@ -730,7 +731,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, p.elem, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW, 32>(s.v, s.tmp, x, slot, g)) / 256.0f;
-        imatrix_weights<32>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
@@ -789,7 +790,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 // d = fp16(scale), levels reprojected at 1/scale with the same LUT rule.
 // One lane per block, 64 blocks per workgroup.
 // ------------------------------------------------------------------
-template <int SRC, bool IMAT>
+template <int SRC, bool IMAT, int SQ>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_iq4_nl(KArgs a) {
     constexpr int BYTES = 18;
     __shared__ __attribute__((aligned(16))) uint8_t stage[64 * BYTES];
@@ -806,7 +807,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, row * a.stride + col, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * cascade8_of<32>([&](int i) { return x[i] * x[i]; })) / 32.0f;
-        imatrix_weights<32>(a.qw + col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, true, SQ>(a.qw + col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];

@@ -117,7 +117,7 @@ def test_sqrt_rounding_option(tmp_path, mode):
     if mode == "ieee":
         oracle.use_ieee_sqrt(True)
     else:
-        oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+        oracle.use_amd_host_sqrt(sqrt_hosts.amd_ulps())
     try:
         check_output(src, out, expect, ftype=30, imatrix=io.load_imatrix(im))
     finally:

@@ -218,7 +218,7 @@ def test_sqrt_rounding_modes(qs, dev, mode, qtype, imat):
     if mode == "ieee":
         oracle.use_ieee_sqrt(True)
     else:
-        oracle.use_sqrt_table(sqrt_hosts.amd_ulps())
+        oracle.use_amd_host_sqrt(sqrt_hosts.amd_ulps())
     try:
         qs.set_sqrt_rounding(mode)
         tid = int(qs.ALL_SPECS[qtype].ggml_type)
