@@ -134,30 +134,52 @@ def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
     return 2 * n_elems + n_elems * OUT_BYTES_PER_256[qtype] // 256 + 4 * k
 
 
+SPIN_CYCLES_PER_S = 2.0e9      # torch.cuda._sleep's clock; measured by spin_rate() at start
+
+
+def spin_rate(torch) -> float:
+    """Clock rate of torch.cuda._sleep's spin kernel on this device (cycles/s)."""
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(1000)
+    a.record(stream)
+    torch.cuda._sleep(2_000_000)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return 2_000_000 / max(1e-6, a.elapsed_time(b) * 1e-3)
+
+
 def time_steps(torch, launches, steps: int, warmup: int):
     """Run `warmup` untimed steps, then time exactly `steps` steps, a step being
     the callables in `launches` (each queues one kernel; called with the step
-    index). Returns (wall ms per step, mean kernel ms per launch slot): an event
-    is recorded on the launch stream before the first and after every launch,
-    so consecutive events bracket one kernel each."""
+    index). Returns (ms per step, mean kernel ms per launch slot), both from
+    events on the launch stream: one before the first launch and one after
+    every launch, so consecutive events bracket one kernel each. The stream is
+    held by a short spin kernel (torch.cuda._sleep) while the timed launches
+    are queued, so kernels shorter than the host's launch cost still run back
+    to back and the brackets hold no host gaps. The hold is not timed."""
     stream = torch.cuda.current_stream()
+    t0 = time.perf_counter()
     for i in range(warmup):
         for f in launches:
             f(i)
+    # host time to queue one launch, from the warm-up (at least 50 us assumed)
+    per_launch_s = max(50e-6, (time.perf_counter() - t0) / max(1, warmup * len(launches)))
     torch.cuda.synchronize()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
           for _ in range(steps)]
-    t0 = time.perf_counter()
+    hold_s = min(2.0, 2.0 * per_launch_s * steps * len(launches) + 2e-3)
+    torch.cuda._sleep(int(hold_s * SPIN_CYCLES_PER_S))
     for i in range(steps):
         ev[i][0].record(stream)
         for j, f in enumerate(launches):
             f(i)
             ev[i][j + 1].record(stream)
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    step_ms = ev[0][0].elapsed_time(ev[-1][-1]) / steps
     per = [sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) / steps
            for j in range(len(launches))]
-    return wall_ms, per
+    return step_ms, per
 
 
 def shape_launches(qs, qtype, imat, xs_rot, qws, outs):
@@ -511,6 +533,8 @@ def main() -> int:
     qs = importlib.import_module("quant-studio_amd")
 
     dev = torch.device("cuda:0")
+    global SPIN_CYCLES_PER_S
+    SPIN_CYCLES_PER_S = spin_rate(torch)
     if args.copy_only:
         return copy_peak(torch, dev, args.steps, args.warmup)
     if args.valu_peak:
