@@ -332,7 +332,7 @@ def device_index(req: Request, ndev: int) -> int:
 
 def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: dict) -> None:
     from . import library, row_bytes, SQRT_ROUNDING
-    from .pipeline import NativePipeline, PipelineError, device_count
+    from .pipeline import NativePipeline, PipelineError, Readahead, device_count
     dev = device_index(req, device_count())
     if req.device in ("cpu", "mps"):
         print(f"note: --device {req.device}: computed on ROCm device {dev} (the same bytes as the "
@@ -359,10 +359,12 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
 
     total_in = total_out = 0
     t0 = time.time()
+    ahead = Readahead([st.tensor for st in steps])
     try:
         with NativePipeline(dev, fd) as pipe:
             for i, (st, info) in enumerate(zip(steps, writer.infos)):
                 t, off = st.tensor, base + info[3]
+                ahead.advance(t.nbytes)
                 if st.dst is None:
                     nbytes = pipe.write(t.data, off)
                 else:
@@ -380,6 +382,8 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
     except PipelineError as e:
         writer.close()
         sys.exit(f"error: {e}")
+    finally:
+        ahead.close()
     os.ftruncate(fd, writer.total_size())     # the trailing padding is zeros
     writer.close()
     print(f"done in {time.time() - t0:.1f}s: {fmt_size(total_in)} -> {fmt_size(total_out)} "

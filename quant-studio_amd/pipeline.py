@@ -31,6 +31,67 @@ class PipelineError(RuntimeError):
     pass
 
 
+class Readahead:
+    """Asks the kernel to read the input tensors into the page cache ahead of
+    the pipeline's copies (madvise MADV_WILLNEED, in plan order, from a
+    thread of its own, a window at a time), at most `budget` bytes past the
+    tensor being queued.
+    The copies fault the mapping in a few MB at a time and the pipeline waits
+    for a free slot between chunks, so with a cold page cache the disk idles
+    between reads; with the requests queued ahead it streams. Best effort:
+    a failing madvise is ignored (the copies fault the pages in anyway)."""
+
+    MADV_WILLNEED = 3
+
+    def __init__(self, tensors: list[TensorInfo], budget: int = 1 << 30, madvise=None):
+        import threading
+        if madvise is None:
+            libc = ctypes.CDLL(None, use_errno=True)
+            libc.madvise.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+            libc.madvise.restype = ctypes.c_int
+            madvise = libc.madvise        # ctypes releases the GIL during the call
+        self._madvise = madvise
+        self._page = os.sysconf("SC_PAGE_SIZE")
+        self._ranges = [(t.data.ctypes.data, t.nbytes) for t in tensors if t.nbytes > 0]
+        self._budget = budget
+        self._queued = 0             # bytes of input the pipeline has been handed so far
+        self._cv = threading.Condition()
+        self._stop = False
+        self._thread = threading.Thread(target=self._run, name="qs-readahead", daemon=True)
+        self._thread.start()
+
+    def advance(self, nbytes: int) -> None:
+        """The pipeline is about to take nbytes more of the input."""
+        with self._cv:
+            self._queued += nbytes
+            self._cv.notify()
+
+    def close(self) -> None:
+        with self._cv:
+            self._stop = True
+            self._cv.notify()
+        self._thread.join()
+
+    WINDOW = 2 << 20         # one request per 2 MiB: the kernel reads at most its
+                             # readahead limit (a few MiB) per madvise call
+
+    def _run(self) -> None:
+        done = 0                 # input bytes advised so far, in plan order
+        for addr, n in self._ranges:
+            a = addr - addr % self._page
+            end = addr + n
+            while a < end:
+                with self._cv:
+                    while not self._stop and done - self._queued > self._budget:
+                        self._cv.wait()
+                    if self._stop:
+                        return
+                w = min(self.WINDOW, end - a)
+                self._madvise(a, w, self.MADV_WILLNEED)
+                done += w
+                a += w
+
+
 def device_count() -> int:
     return int(library().qs_device_count())
 

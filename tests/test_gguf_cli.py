@@ -209,3 +209,58 @@ def test_shape_fallback_types(tmp_path, scheme, want):
     for short, t in want.items():
         assert lines[f"blk.0.{short}.weight"][3] == t, (short, lines[f"blk.0.{short}.weight"])
     assert "falling back to" in r.stderr
+
+
+def test_readahead_walks_the_plan_within_its_budget(tmp_path):
+    """The input readahead advises the mapped tensors in plan order (page-aligned
+    starts), stays within its byte budget of what the pipeline has taken, and
+    stops cleanly when closed while waiting; the real madvise accepts its
+    arguments on a mapped file (CPU only)."""
+    import mmap
+    import threading
+    import time
+    pipeline = importlib.import_module("quant-studio_amd.pipeline")
+    path = tmp_path / "blob.bin"
+    path.write_bytes(bytes(range(256)) * 4096)               # 1 MiB
+    with open(path, "rb") as f:
+        mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+        base = np.frombuffer(mm, dtype=np.uint8)
+        ts = [io.TensorInfo(f"t{i}", (1024,), GT.BF16, 0, 2048, base[i * 4096 + 7: i * 4096 + 7 + 2048])
+              for i in range(200)]
+        ra = pipeline.Readahead(ts[:4])                       # the libc madvise, on real pages
+        for t in ts[:4]:
+            ra.advance(t.nbytes)
+        ra.close()
+        advised, lock = [], threading.Lock()
+
+        def record(a, n, adv):
+            with lock:
+                advised.append((a, n, adv))
+            return 0
+
+        page = pipeline.os.sysconf("SC_PAGE_SIZE")
+        ra = pipeline.Readahead(ts, budget=16 * 1024, madvise=record)
+        time.sleep(0.2)
+        first = len(advised)
+        assert 0 < first <= 16 * 1024 // 2048 + 1             # stopped at the budget
+        for t in ts[:50]:
+            ra.advance(t.nbytes)
+        time.sleep(0.2)
+        assert first < len(advised) <= 50 + 16 * 1024 // 2048 + 1
+        ra.close()                                             # ends while waiting
+        starts = [a for a, _, _ in advised]
+        assert starts == sorted(starts)
+        assert all(adv == pipeline.Readahead.MADV_WILLNEED for _, _, adv in advised)
+        addr0 = ts[0].data.ctypes.data
+        assert advised[0] == (addr0 - addr0 % page, 2048 + addr0 % page, 3)
+        # a tensor longer than the window is advised window by window, in order
+        big = [io.TensorInfo("big", (1 << 19,), GT.BF16, 0, 1 << 20, base[4096 + 5: 4096 + 5 + (1 << 20)])]
+        win = []
+        ra2 = type("R", (pipeline.Readahead,), {"WINDOW": 1 << 18})(
+            big, madvise=lambda a, n, adv: win.append((a, n)) or 0)
+        time.sleep(0.2)
+        ra2.close()
+        a0 = big[0].data.ctypes.data
+        assert win[0][0] == a0 - a0 % page and all(n == 1 << 18 for _, n in win[:-1])
+        assert sum(n for _, n in win) == (1 << 20) + a0 % page
+        assert all(win[i + 1][0] == win[i][0] + win[i][1] for i in range(len(win) - 1))
