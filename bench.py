@@ -447,10 +447,11 @@ def drop_page_cache(path: Path) -> None:
         os.close(fd)
 
 
-def run_e2e(torch, dev, schemes: list[str], where: str | None) -> int:
+def e2e_runs(torch, dev, schemes: list[str], where: str | None) -> dict:
     """The command line on the synthetic model, per scheme: one run with the
     input in the page cache (warm) and one after evicting the input and the
-    imatrix from it (cold; only meaningful on a disk-backed filesystem)."""
+    imatrix from it (cold; only meaningful on a disk-backed filesystem).
+    Returns the record (raises on a failed run)."""
     import re
     import subprocess
     import tempfile
@@ -478,8 +479,7 @@ def run_e2e(torch, dev, schemes: list[str], where: str | None) -> int:
                 r = subprocess.run(cmd, capture_output=True, text=True)
                 wall = time.perf_counter() - t0
                 if r.returncode != 0:
-                    print(r.stderr[-2000:], file=sys.stderr)
-                    return 1
+                    raise RuntimeError(f"e2e {sch}: the command line failed:\n{r.stderr[-2000:]}")
                 m = re.search(r"done in ([0-9.]+)s", r.stdout)
                 pipe_s = float(m.group(1)) if m else None
                 results[f"{sch} {cache}"] = {
@@ -489,12 +489,16 @@ def run_e2e(torch, dev, schemes: list[str], where: str | None) -> int:
                     "out_bytes": out.stat().st_size}
                 out.unlink()
                 print(f"e2e {sch} {cache}: {results[f'{sch} {cache}']}", file=sys.stderr, flush=True)
-        print(json.dumps({"e2e": "synthetic 4B-class bf16 GGUF (36 layers, 2560/9728, vocab 151936)",
-                          "filesystem": fs_type(d), "file_bytes": src.stat().st_size,
-                          "weights": n, "generate_s": round(gen_s, 1),
-                          "cold": "input and imatrix evicted from the page cache before the run "
-                                  "(fsync + POSIX_FADV_DONTNEED)",
-                          "runs": results}), flush=True)
+        return {"e2e": "synthetic 4B-class bf16 GGUF (36 layers, 2560/9728, vocab 151936)",
+                "filesystem": fs_type(d), "file_bytes": src.stat().st_size,
+                "weights": n, "generate_s": round(gen_s, 1),
+                "cold": "input and imatrix evicted from the page cache before the run "
+                        "(fsync + POSIX_FADV_DONTNEED)",
+                "runs": results}
+
+
+def run_e2e(torch, dev, schemes: list[str], where: str | None) -> int:
+    print(json.dumps(e2e_runs(torch, dev, schemes, where)), flush=True)
     return 0
 
 
@@ -515,6 +519,9 @@ def main() -> int:
     ap.add_argument("--e2e", default=None,
                     help="run the CLI end to end on a synthetic 4B-class model for these "
                          "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M') and print its own JSON line")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the default end-to-end leg (the command line on the synthetic "
+                         "4B-class model, IQ2_XXS warm and cold)")
     ap.add_argument("--e2e-dir", default=None, help="directory for the e2e model (default: the "
                     "first disk-backed of $TMPDIR, /tmp, /var/tmp, the repository)")
     ap.add_argument("--valu-peak", action="store_true",
@@ -649,6 +656,15 @@ def main() -> int:
         line["cpu_baseline"] = cb
         head = cb["per_type"].get("q4_k+imat")
         line["identical_pct_vs_oracle"] = None if head is None else head["identical_pct"]
+    if not args.no_e2e:
+        # the command line end to end on the synthetic 4B-class model (BASELINE
+        # configs 3 and the full-model IQ2_XXS run), warm and cold page cache;
+        # supplementary to the headline, so a failure is reported in the line
+        try:
+            line["e2e"] = e2e_runs(torch, dev, ["IQ2_XXS", "Q4_K_M --mem 4G"], args.e2e_dir)
+        except Exception as e:
+            print(f"bench: e2e leg failed: {e}", file=sys.stderr, flush=True)
+            line["e2e"] = {"error": str(e)[-500:]}
     print(json.dumps(line), flush=True)
     return 0
 
