@@ -129,6 +129,31 @@ def valu_peak(torch, dev, launches: int = 5) -> float:
     return lib.qs_calib_valu_insts(grid, iters) / sec
 
 
+def copy_kernel_peak(torch, dev, nbytes: int = 1 << 30, launches: int = 10) -> float:
+    """Measured copy rate (read + written bytes per second) of a streaming
+    16-byte copy kernel shaped like the 32-value quantizer (libqs_calib.so),
+    1 GiB each way, launches back to back."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "quant-studio_amd" / "_build" / "libqs_calib.so"))
+    lib.qs_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    stream = torch.cuda.current_stream()
+    run = lambda: lib.qs_calib_copy(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                                    nbytes, ctypes.c_void_p(stream.cuda_stream))
+    assert run() == 0
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(launches):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / launches
+    del a, b
+    return 2 * nbytes / sec
+
+
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
     """bf16 in + packed blocks out + the imatrix (4k bytes)."""
     return 2 * n_elems + n_elems * OUT_BYTES_PER_256[qtype] // 256 + 4 * k
@@ -573,6 +598,7 @@ def main() -> int:
     insts = profile_figure("counters_q4_k_imat_9728x2560.md", "valu_insts_per_launch")
     traffic = profile_figure("counters_q4_k_imat_9728x2560.md", "traffic_bytes_per_launch")
     peak_valu = valu_peak(torch, dev)
+    copy_peak_gbs = copy_kernel_peak(torch, dev) / 1e9
 
     per_type, gpu_out = {}, {}
     valu_counts = profiled_valu_per_type()
@@ -591,6 +617,7 @@ def main() -> int:
                 "ms_per_step": round(st, 4),
                 "kernel_ms": [round(v, 4) for v in km],
                 "hbm_frac": round(a / HBM_PEAK_GBS, 4),
+                "copy_frac": round(a / copy_peak_gbs, 4),
                 # VALU issue rate (SQ_INSTS_VALU per launch over the live launch
                 # time) against the calibration kernel's rate
                 "valu_frac": None if n_insts is None else
@@ -609,6 +636,9 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "q4_0" in sel:
         per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
+    for row in [per_type.get("q4_0 token_embd 151936x2560"), configs.get("c1_q4_0_4096x4096")]:
+        if row:
+            row["copy_frac"] = round(row["hbm_frac"] * HBM_PEAK_GBS / copy_peak_gbs, 4)
 
     line = {
         "metric": "input GB/s (bf16) per quant type at 1 GPU + % identical blocks vs reference",
@@ -641,6 +671,9 @@ def main() -> int:
                          "achieved": round(insts / (kms[0] * 1e-3) / 1e9, 1),
                          "peak": round(peak_valu / 1e9, 1),
                          "frac": round(insts / (kms[0] * 1e-3) / peak_valu, 4)}},
+        "copy_peak": {"GBps": round(copy_peak_gbs, 1), "unit": "GB/s read + written",
+                      "kernel": "k_copy_stream (libqs_calib.so), 1 GiB, 16-byte non-temporal "
+                                "loads and stores, 10 launches back to back"},
         "per_type": per_type,
         "configs": configs,
     }
