@@ -156,9 +156,9 @@ QS_DEV float sqrt_ref(float v, const SqrtMap& m) {
 }
 
 // sqrt_ref over a lane's N values, every map load issued before any is used.
-// BAND reads the maps only where sqrt_lookup_key asks; without it every value
-// reads its own words, which keeps fewer registers live: the Q4_K/Q5_K
-// kernels measured 1-2% faster that way, the others 2-17% slower.
+// BAND reads the maps only where sqrt_lookup_key asks (every kernel uses it:
+// 2-17% faster where the map loads were on the critical path, as fast for
+// Q4_K/Q5_K); without it every value reads its own words.
 template <int N, bool BAND, int SQ>
 QS_DEV void sqrt_ref_n(const float (&v)[N], const SqrtMap& m, float (&out)[N]) {
     if constexpr (SQ == SQ_IEEE) {

@@ -329,7 +329,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4
         wave_sync();
         const float sum = sb_cascade8_256<LPS>(s.v[slot], s.tmp[slot], g);
         const float sigma2 = (2.0f * sum) / 256.0f;
-        imatrix_weights<32, false, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
         float t[32];
 #pragma unroll
