@@ -13,7 +13,9 @@ the step time come from the same launches.
 
 The JSON line also carries:
   - per_type: every HIP type with and without imatrix on the same shapes:
-    kernel GB/s, HBM-roofline fraction and VALU fraction;
+    kernel GB/s, HBM-roofline fraction and VALU fraction; the 32-value
+    formats also against a copy kernel (at 1 GiB, and moving the same bytes
+    per launch: the ceiling of a launch that size);
   - configs: Q4_0 on one 4096x4096 bf16 tensor with 0.1% outliers (seed 0),
     and IQ2_XXS + imatrix on 36 heavy-tailed (Student-t, df 5) 2560x9728
     ffn_down tensors, each timed as its own workload;
@@ -52,6 +54,7 @@ TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 1
             "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
 NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
 IGNORE_IMATRIX = {"q4_0", "q4_1", "q5_0", "q5_1", "q8_0"}
+B32_TYPES = IGNORE_IMATRIX          # the 32-value formats: HBM-bound, compared with a copy
 BLOCK_VALUES = {t: (32 if t in IGNORE_IMATRIX | {"iq4_nl"} else 256) for t in OUT_BYTES_PER_256}
 BLOCK_BYTES = {t: OUT_BYTES_PER_256[t] * BLOCK_VALUES[t] // 256 for t in OUT_BYTES_PER_256}
 SHAPES = [(9728, 2560), (2560, 9728)]   # (rows, k)
@@ -129,13 +132,19 @@ def valu_peak(torch, dev, launches: int = 5) -> float:
     return lib.qs_calib_valu_insts(grid, iters) / sec
 
 
+def _calib_lib():
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "quant-studio_amd" / "_build" / "libqs_calib.so"))
+    lib.qs_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    return lib
+
+
 def copy_kernel_peak(torch, dev, nbytes: int = 1 << 30, launches: int = 10) -> float:
     """Measured copy rate (read + written bytes per second) of a streaming
     16-byte copy kernel shaped like the 32-value quantizer (libqs_calib.so),
     1 GiB each way, launches back to back."""
     import ctypes
-    lib = ctypes.CDLL(str(ROOT / "quant-studio_amd" / "_build" / "libqs_calib.so"))
-    lib.qs_calib_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    lib = _calib_lib()
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
     stream = torch.cuda.current_stream()
@@ -152,6 +161,31 @@ def copy_kernel_peak(torch, dev, nbytes: int = 1 << 30, launches: int = 10) -> f
     sec = e0.elapsed_time(e1) * 1e-3 / launches
     del a, b
     return 2 * nbytes / sec
+
+
+def copy_kernel_rate(torch, dev, traffic: int, steps: int = 24) -> float:
+    """Read + written bytes per second of the same copy kernel when one launch
+    moves `traffic` bytes (half read, half written): the ceiling of a launch of
+    that size, ramp-up and drain included. Buffer pairs rotate over >= 1 GiB so
+    the MALL holds none of them; launches run back to back (time_steps)."""
+    import ctypes
+    lib = _calib_lib()
+    n = max(16, traffic // 2 // 16 * 16)
+    pairs = max(2, -(-(1 << 30) // (2 * n)))
+    bufs = [(torch.empty(n, dtype=torch.uint8, device=dev).fill_(1),
+             torch.empty(n, dtype=torch.uint8, device=dev)) for _ in range(pairs)]
+    stream = torch.cuda.current_stream()
+
+    def launch(i):
+        a, b = bufs[i % pairs]
+        rc = lib.qs_calib_copy(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()), n,
+                               ctypes.c_void_p(stream.cuda_stream))
+        if rc:
+            raise RuntimeError(f"qs_calib_copy failed ({rc})")
+    _, per = time_steps(torch, [launch], steps, 5)
+    del bufs
+    torch.cuda.empty_cache()
+    return 2 * n / (per[0] * 1e-3)
 
 
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
@@ -376,7 +410,10 @@ def q4_0_large(torch, qs, dev, steps: int) -> dict:
 
 
 def copy_peak(torch, dev, steps: int, warmup: int) -> int:
-    """1 GiB device-to-device copy: measured HBM copy rate (read + write bytes)."""
+    """1 GiB device-to-device copy (torch's copy kernel: the reference size for
+    scaling the FETCH_SIZE / WRITE_SIZE counters), then the streaming copy
+    kernel's rate per launch size: the launches of the Q4_0 workloads (4096x4096,
+    one 9728x2560 ffn tensor, the 151936x2560 token_embd) and 1 GiB each way."""
     nbytes = 1 << 30
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
@@ -385,6 +422,17 @@ def copy_peak(torch, dev, steps: int, warmup: int) -> int:
                       "ms_per_copy": round(per[0], 4),
                       "copy_GBps_read_plus_write": round(2 * nbytes / (per[0] * 1e-3) / 1e9, 1)}),
           flush=True)
+    del a, b
+    torch.cuda.empty_cache()
+    for name, traffic in [("q4_0 4096x4096", algorithmic_bytes("q4_0", 4096 * 4096, 4096) - 4 * 4096),
+                          ("q4_0 9728x2560", algorithmic_bytes("q4_0", 9728 * 2560, 2560) - 4 * 2560),
+                          ("q4_0 151936x2560", algorithmic_bytes("q4_0", 151936 * 2560, 2560) - 4 * 2560),
+                          ("1 GiB each way", 2 << 30)]:
+        r = copy_kernel_rate(torch, dev, traffic)
+        print(json.dumps({"stream_copy_bytes_per_launch": traffic, "as_the_launch_of": name,
+                          "us_per_launch": round(traffic / r * 1e6, 2),
+                          "GBps_read_plus_write": round(r / 1e9, 1),
+                          "frac_of_8TBps": round(r / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
     return 0
 
 
@@ -602,6 +650,13 @@ def main() -> int:
 
     per_type, gpu_out = {}, {}
     valu_counts = profiled_valu_per_type()
+    copy_rates = {}
+
+    def same_size_copy(traffic: int) -> float:
+        """GB/s of the copy kernel at this traffic per launch (measured once per size)."""
+        if traffic not in copy_rates:
+            copy_rates[traffic] = copy_kernel_rate(torch, dev, traffic) / 1e9
+        return copy_rates[traffic]
     sel = [] if args.types == "none" else (list(TYPE_IDS) if args.types == "all"
                                            else args.types.split(","))
     for qtype in sel:
@@ -618,6 +673,11 @@ def main() -> int:
                 "kernel_ms": [round(v, 4) for v in km],
                 "hbm_frac": round(a / HBM_PEAK_GBS, 4),
                 "copy_frac": round(a / copy_peak_gbs, 4),
+                # against the copy kernel moving this launch's bytes (the
+                # ceiling of a launch this size, ramp-up and drain included)
+                "copy_frac_same_size": round(a / same_size_copy(
+                    algorithmic_bytes(qtype, SHAPES[0][0] * SHAPES[0][1], SHAPES[0][1])), 4)
+                if qtype in B32_TYPES else None,
                 # VALU issue rate (SQ_INSTS_VALU per launch over the live launch
                 # time) against the calibration kernel's rate
                 "valu_frac": None if n_insts is None else
@@ -636,9 +696,13 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "q4_0" in sel:
         per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
-    for row in [per_type.get("q4_0 token_embd 151936x2560"), configs.get("c1_q4_0_4096x4096")]:
+    for row, alg_b in [(per_type.get("q4_0 token_embd 151936x2560"),
+                        algorithmic_bytes("q4_0", 151936 * 2560, 2560) - 4 * 2560),
+                       (configs.get("c1_q4_0_4096x4096"),
+                        algorithmic_bytes("q4_0", 4096 * 4096, 4096) - 4 * 4096)]:
         if row:
             row["copy_frac"] = round(row["hbm_frac"] * HBM_PEAK_GBS / copy_peak_gbs, 4)
+            row["copy_frac_same_size"] = round(row["hbm_frac"] * HBM_PEAK_GBS / same_size_copy(alg_b), 4)
 
     line = {
         "metric": "input GB/s (bf16) per quant type at 1 GPU + % identical blocks vs reference",
