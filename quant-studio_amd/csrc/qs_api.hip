@@ -255,8 +255,10 @@ const T* upload(const std::vector<T>& v) {
     void* p = nullptr;
     const size_t n = std::max<size_t>(1, v.size()) * sizeof(T);
     if (hipMalloc(&p, n) != hipSuccess) return nullptr;
-    if (!v.empty() && hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess)
+    if (!v.empty() && hipMemcpy(p, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipFree(p);
         return nullptr;
+    }
     return static_cast<const T*>(p);
 }
 
@@ -289,7 +291,12 @@ bool device_tables_locked(int dev, int iq_table, const std::array<bool, SQM_N>& 
         g.cinfo = upload(h.cinfo);
         g.nbr = upload(h.nbr);
         g.code0 = h.code0;
-        if (!h.ok || !g.grid || !g.cinfo || !g.nbr) return false;
+        if (!h.ok || !g.grid || !g.cinfo || !g.nbr) {
+            // nothing is kept from a failed upload; the next call tries again
+            for (const void* q : {(const void*)g.grid, (const void*)g.cinfo, (const void*)g.nbr})
+                if (q) (void)hipFree(const_cast<void*>(q));
+            return false;
+        }
         d.iq[iq_table] = g;
     }
     out = d;
