@@ -669,11 +669,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
 // IQ3_XXS / IQ3_S  quantize_iq3_xxs iq3_xxs.py:31-134, quantize_iq3_s
 // iq3_s.py:31-140
 // ------------------------------------------------------------------
+
+
+// IQ3_XXS / IQ3_S (iq3_common.py:209-256, iq3_xxs.py:31-134, iq3_s.py:31-140)
+// with a lane pair per 32-value group: each lane holds 16 values (subgroups
+// 4h..4h+3 of its half h), so a wave takes 4 superblocks and each subgroup
+// pass searches one list per lane. The group's sums are the two halves'
+// trees joined by one exchange: the reference's tree over the 8 subgroup sums
+// is ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)), and fl(a + b) = fl(b + a), so
+// both lanes hold the same bit-exact sums and take the same accept
+// decisions. Against one lane per group (32 values, 8 superblocks per wave):
+// 125-128 VGPRs and 4 waves per SIMD instead of 168 with 59-64 spilled at 3
+// waves (IQ3_S with imatrix: 2 waves), IQ3_XXS 15%, IQ3_S 17%, IQ3_S with
+// imatrix 25% faster; 5 waves spill and are slower.
 template <int SRC, bool IS_S, bool IMAT, int SQ>
-// 3 waves per SIMD where it pays (IQ3_XXS 22%, IQ3_S without imatrix 12%
-// faster than 2); IQ3_S with imatrix spills too much at 3 and keeps 2
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT ? 2 : 3))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
-    constexpr int LPS = 8, SPW = 8, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
+    constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
+    constexpr int SMASK = IS_S ? 255 : 127;
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ __align__(16) uint32_t glds[GS];
     __shared__ int act_lds[SPW][8];
@@ -681,50 +693,58 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT
     __shared__ uint8_t cmap[64 * MAXCH];
     __shared__ unsigned long long res[64];
     stage_levels<3, 4, GS>(T.grid, glds);
-    const SbPos p = sb_pos<LPS, 32>(a.n_units, a.units_per_row, a.stride);
-    const int slot = p.slot, g = p.g;
-    float x[32], w[32], waux[32], xval[32];
-    iq_load_weights<SRC, LPS, 32, SQ>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
-    sqrt_ref_n<32, true, SQ>(w, a.sqrt, waux);
+    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, grp = p.g >> 1, half = p.g & 1;
+    float x[16], w[16], waux[16], xval[16];
+    iq_load_weights<SRC, LPS, 16, SQ>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
+    sqrt_ref_n<16, true, SQ>(w, a.sqrt, waux);
     keep_in_registers(waux);
-    int signs[4];
+    int signs[2];
     if constexpr (IS_S) {
-        static_for<0, 4>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });
+        static_for<0, 2>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });
     } else {
-        static_for<0, 4>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
+        static_for<0, 2>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
     }
     float gmax = xval[0];
 #pragma unroll
-    for (int i = 1; i < 32; i++) gmax = fmaxf(gmax, xval[i]);
+    for (int i = 1; i < 16; i++) gmax = fmaxf(gmax, xval[i]);
+    gmax = fmaxf(gmax, __shfl_xor(gmax, 1));
     const bool active = IS_S ? gmax > 0 : gmax >= 1e-8f;
     const float gsafe = active ? gmax : 1.0f;
     float scale = gmax / 15.0f, best = 0.0f;
-    int Wg[8];
-    bool og[8];
+    int Wg[4];
+    bool og[4];
 #pragma unroll
-    for (int k = 0; k < 8; k++) {
+    for (int k = 0; k < 4; k++) {
         Wg[k] = 0;
         og[k] = !IS_S;
     }
+    // the group's two sums: this lane's half-tree joined with the partner's
+    auto group_sums = [&](const int (&gi)[4], float& sumqx, float& sumq2) {
+        float hx, h2;
+        iq_tree_sums<3, 4, 4>(glds, gi, w, xval, hx, h2);
+        sumqx = hx + __shfl_xor(hx, 1);
+        sumq2 = h2 + __shfl_xor(h2, 1);
+    };
     wave_sync();   // glds ready
 #pragma unroll 1
     for (int st = 0; st < steps.n; st++) {
         const float inv = rdiv(steps.v[st], gsafe), sc = 1.0f / inv;
-        int gi[8];
-        bool on[8];
-        uint32_t ci[8];
-        iq_codes<3, 4, 8>(T, xval, inv, ci);
-        static_for<0, 8>([&](auto S) {
+        int gi[4];
+        bool on[4];
+        uint32_t ci[4];
+        iq_codes<3, 4, 4>(T, xval, inv, ci);
+        static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
         float sumqx, sumq2;
-        iq_tree_sums<3, 4, 8>(glds, gi, w, xval, sumqx, sumq2);
+        group_sums(gi, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
             const float ns = sumqx / fmaxf(sumq2, F32_TINY);
             scale = ns;
             best = ns * sumqx;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
+            for (int k = 0; k < 4; k++) {
                 Wg[k] = gi[k];
                 og[k] = on[k];
             }
@@ -732,73 +752,82 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S && IMAT
     }
     bool anyoff = false;
 #pragma unroll
-    for (int k = 0; k < 8; k++) anyoff = anyoff || !og[k];
+    for (int k = 0; k < 4; k++) anyoff = anyoff || !og[k];
+    // the exchange runs in every lane (behind `||` it would run only where
+    // anyoff is false and read inactive partners)
+    const int partner_off = __shfl_xor((int)anyoff, 1);
+    anyoff = anyoff || partner_off != 0;
     const bool redo = active && anyoff && scale > 0;
     {
         const float inv2 = 1.0f / (redo ? scale : 1.0f);
-        int w2[8];
-        bool on[8];
-        uint32_t ci[8];
-        iq_codes<3, 4, 8>(T, xval, inv2, ci);
-        static_for<0, 8>([&](auto S) {
+        int w2[4];
+        bool on[4];
+        uint32_t ci[4];
+        iq_codes<3, 4, 4>(T, xval, inv2, ci);
+        static_for<0, 4>([&](auto S) {
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);
         });
 #pragma unroll
-        for (int k = 0; k < 8; k++)
+        for (int k = 0; k < 4; k++)
             if (redo && (IS_S || !og[k])) Wg[k] = w2[k];
         float sumqx, sumq2;
-        iq_tree_sums<3, 4, 8>(glds, Wg, w, xval, sumqx, sumq2);
+        group_sums(Wg, sumqx, sumq2);
         if (redo && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
     }
     if (active && scale < 0) {
         scale = -scale;
 #pragma unroll
-        for (int k = 0; k < 4; k++) signs[k] = (~signs[k]) & (IS_S ? 255 : 127);
+        for (int k = 0; k < 2; k++) signs[k] = (~signs[k]) & SMASK;
     }
-    s.sc[slot][g] = active ? scale : 0.0f;
-    act_lds[slot][g] = active ? 1 : 0;
+    if (half == 0) {
+        s.sc[slot][grp] = active ? scale : 0.0f;
+        act_lds[slot][grp] = active ? 1 : 0;
+    }
     uint8_t* o = s.out + slot * BYTES;
-    for (int t = g; t < BYTES; t += LPS) o[t] = 0;
+    for (int t = p.g; t < BYTES; t += LPS) o[t] = 0;
     wave_sync();
     float d;
     bool has;
     int l[8];
     iq_scale_nibbles<8>(s.sc[slot], d, has, l);
     if constexpr (!IS_S) {
-        if (g == 0) {
+        if (p.g == 0) {
             const uint32_t h = f16_bits(has ? d * 1.0125f : 0.0f);
             o[0] = (uint8_t)h;
             o[1] = (uint8_t)(h >> 8);
         }
-        uint32_t word = 0;
+        // sign word of the group: 7 bits per 8-value chunk, chunks 2h, 2h+1 here
+        uint32_t part = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) word |= (uint32_t)(active ? signs[k] : 0) << (7 * k);
-        word |= (uint32_t)l[g] << 28;
+        for (int k = 0; k < 2; k++) part |= (uint32_t)(active ? signs[k] : 0) << (7 * (2 * half + k));
+        uint32_t word = part | (uint32_t)__shfl_xor((int)part, 1);
+        word |= (uint32_t)l[grp] << 28;
         if (!has) word = 0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) o[2 + 8 * g + k] = (uint8_t)((has && active) ? Wg[k] : 0);
+        for (int k = 0; k < 4; k++) o[2 + 8 * grp + 4 * half + k] = (uint8_t)((has && active) ? Wg[k] : 0);
 #pragma unroll
-        for (int k = 0; k < 4; k++) o[66 + 4 * g + k] = (uint8_t)(word >> (8 * k));
+        for (int k = 0; k < 2; k++) o[66 + 4 * grp + 2 * half + k] = (uint8_t)(word >> (8 * (2 * half + k)));
     } else {
-        if (g == 0) {
+        if (p.g == 0) {
             const uint32_t h = f16_bits(has ? d * 1.033f : 0.0f);
             o[0] = (uint8_t)h;
             o[1] = (uint8_t)(h >> 8);
         }
-        int h = 0;
+        int hb = 0;
 #pragma unroll
-        for (int k = 0; k < 8; k++) h |= (Wg[k] >> 8) << k;
-        o[66 + g] = (uint8_t)(active ? h : 0);
+        for (int k = 0; k < 4; k++) hb |= (Wg[k] >> 8) << (4 * half + k);
+        hb |= __shfl_xor(hb, 1);
+        if (half == 0) o[66 + grp] = (uint8_t)(active ? hb : 0);
         if (active) {
             int slot_idx = 0;                  // live groups compact to the front (iq3_s.py:113-122)
-            for (int j = 0; j < g; j++) slot_idx += act_lds[slot][j];
+            for (int j = 0; j < grp; j++) slot_idx += act_lds[slot][j];
 #pragma unroll
-            for (int k = 0; k < 8; k++) o[2 + 8 * slot_idx + k] = (uint8_t)(Wg[k] & 255);
+            for (int k = 0; k < 4; k++) o[2 + 8 * slot_idx + 4 * half + k] = (uint8_t)(Wg[k] & 255);
 #pragma unroll
-            for (int k = 0; k < 4; k++) o[74 + 4 * slot_idx + k] = (uint8_t)signs[k];
+            for (int k = 0; k < 2; k++) o[74 + 4 * slot_idx + 2 * half + k] = (uint8_t)signs[k];
         }
-        if (g < 4) o[106 + g] = (uint8_t)(has ? (l[2 * g] | (l[2 * g + 1] << 4)) : 0);
+        if (p.g < 4) o[106 + p.g] = (uint8_t)(has ? (l[2 * p.g] | (l[2 * p.g + 1] << 4)) : 0);
     }
     wave_sync();
     sb_store(s, a);
