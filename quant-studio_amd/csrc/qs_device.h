@@ -193,21 +193,29 @@ QS_DEV void sqrt_ref_n(const float (&v)[N], const SqrtMap& m, float (&out)[N]) {
 }
 
 // imatrix weights w[i] = qw[i] * sqrt_ref(sigma2 + x[i]^2) (e.g. q4_k.py:51),
-// with the imatrix and map loads issued together
-template <int N, bool BAND, int SQ>
+// with the imatrix and map loads of CH values issued together (CH < N bounds
+// the registers the phase holds, for kernels whose occupancy it would set)
+template <int N, bool BAND, int SQ, int CH = N>
 QS_DEV void imatrix_weights(const float* __restrict__ qw, float sigma2, const float (&x)[N],
                             const SqrtMap& m, float (&w)[N]) {
-    float v[N], q[N];
+    static_assert(N % CH == 0, "chunks tile the group");
 #pragma unroll
-    for (int i = 0; i < N; i++) {
-        const float t = x[i] * x[i];
-        v[i] = sigma2 + t;
-        q[i] = qw[i];
+    for (int c = 0; c < N; c += CH) {
+        float v[CH], q[CH];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const float t = x[c + i] * x[c + i];
+            v[i] = sigma2 + t;
+            q[i] = qw[c + i];
+        }
+        float r[CH];
+        sqrt_ref_n<CH, BAND, SQ>(v, m, r);
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            w[c + i] = q[i] * r[i];
+            if constexpr (CH < N) keep_in_register(w[c + i]);
+        }
     }
-    float r[N];
-    sqrt_ref_n<N, BAND, SQ>(v, m, r);
-#pragma unroll
-    for (int i = 0; i < N; i++) w[i] = q[i] * r[i];
 }
 
 // f32 -> fp16 bits, round to nearest even (v_cvt_f16_f32 under the default mode)

@@ -731,13 +731,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, p.elem, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * sb_sumsq_halves<LPS, SPW, 32>(s.v, s.tmp, x, slot, g)) / 256.0f;
-        imatrix_weights<32, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, true, SQ, 8>(a.qw + p.col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
     }
     if constexpr (!IMAT) wave_sync();          // iq4tab ready (the imatrix path synced above)
-    const float scale = iq4_scale_search(x, w, iq4tab);
+    const float scale = iq4_scale_search<IMAT ? 16 : 32>(x, w, iq4tab);
     s.sc[slot][g] = scale;
     wave_sync();
     float sc8[8];
@@ -807,13 +807,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
     load_elems<SRC, true, 32>(a.src, row * a.stride + col, x);
     if constexpr (IMAT) {
         const float sigma2 = (2.0f * cascade8_of<32>([&](int i) { return x[i] * x[i]; })) / 32.0f;
-        imatrix_weights<32, true, SQ>(a.qw + col, sigma2, x, a.sqrt, w);
+        imatrix_weights<32, true, SQ, 8>(a.qw + col, sigma2, x, a.sqrt, w);
     } else {
 #pragma unroll
         for (int i = 0; i < 32; i++) w[i] = x[i] * x[i];
     }
     wave_sync();                                 // iq4tab ready
-    const float scale = iq4_scale_search(x, w, iq4tab);
+    const float scale = iq4_scale_search<IMAT ? 16 : 32>(x, w, iq4tab);
     const float id = scale != 0.0f ? 1.0f / scale : 0.0f;
     uint8_t* o = stage + lane * BYTES;
     const uint32_t h = f16_bits(scale);
