@@ -671,20 +671,24 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
 // ------------------------------------------------------------------
 
 
+
 // IQ3_XXS / IQ3_S (iq3_common.py:209-256, iq3_xxs.py:31-134, iq3_s.py:31-140)
-// with a lane pair per 32-value group: each lane holds 16 values (subgroups
-// 4h..4h+3 of its half h), so a wave takes 4 superblocks and each subgroup
-// pass searches one list per lane. The group's sums are the two halves'
-// trees joined by one exchange: the reference's tree over the 8 subgroup sums
-// is ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)), and fl(a + b) = fl(b + a), so
-// both lanes hold the same bit-exact sums and take the same accept
-// decisions. Against one lane per group (32 values, 8 superblocks per wave):
-// 125-128 VGPRs and 4 waves per SIMD instead of 168 with 59-64 spilled at 3
-// waves (IQ3_S with imatrix: 2 waves), IQ3_XXS 15%, IQ3_S 17%, IQ3_S with
-// imatrix 25% faster; 5 waves spill and are slower.
-template <int SRC, bool IS_S, bool IMAT, int SQ>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
-    constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
+// with LPG lanes per 32-value group: each lane holds 32/LPG values (its
+// subgroups of 4), a wave takes 8/LPG superblocks and each subgroup pass
+// searches one list per lane. The group's sums are the lanes' trees joined
+// by a butterfly of lane exchanges: the reference's tree over the 8 subgroup
+// sums is ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)), each exchange level joins
+// two adjacent subtrees, and fl(a + b) = fl(b + a), so every lane of the
+// group holds the same bits and takes the same accept and re-projection
+// decisions (the maximum, the off-grid flag and the packed sign and high-bit
+// words are joined the same way). Measured against one lane per group (168
+// VGPRs with 59-64 spilled at 3 waves per SIMD; IQ3_S with imatrix at 2):
+// LPG = 2 (125-128 VGPRs, 4 waves) IQ3_XXS 15%, IQ3_S 17%, IQ3_S with
+// imatrix 25% faster; LPG = 4 (80 VGPRs, 6 waves) another 5-6.5%; same bytes.
+template <int SRC, bool IS_S, bool IMAT, int SQ, int LPG>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6 : 4))) void k_iq3(KArgs a, IqTabDev T, IqSteps steps) {
+    constexpr int VPL = 32 / LPG, NSL = VPL / 4, NCH = VPL / 8;
+    constexpr int LPS = 8 * LPG, SPW = 64 / LPS, BYTES = IS_S ? 110 : 98, GS = IS_S ? 512 : 256;
     constexpr int SMASK = IS_S ? 255 : 127;
     __shared__ IqLds<SPW, BYTES> s;
     __shared__ __align__(16) uint32_t glds[GS];
@@ -693,48 +697,53 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     __shared__ uint8_t cmap[64 * MAXCH];
     __shared__ unsigned long long res[64];
     stage_levels<3, 4, GS>(T.grid, glds);
-    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
-    const int slot = p.slot, grp = p.g >> 1, half = p.g & 1;
-    float x[16], w[16], waux[16], xval[16];
-    iq_load_weights<SRC, LPS, 16, SQ>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
-    sqrt_ref_n<16, true, SQ>(w, a.sqrt, waux);
+    const SbPos p = sb_pos<LPS, VPL>(a.n_units, a.units_per_row, a.stride);
+    const int slot = p.slot, grp = p.g / LPG, q = p.g % LPG;
+    float x[VPL], w[VPL], waux[VPL], xval[VPL];
+    iq_load_weights<SRC, LPS, VPL, SQ>(a, p, s.v, s.tmp, 2.0f, !IMAT, x, w);
+    sqrt_ref_n<VPL, true, SQ>(w, a.sqrt, waux);
     keep_in_registers(waux);
-    int signs[2];
+    int signs[NCH];
     if constexpr (IS_S) {
-        static_for<0, 2>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });
+        static_for<0, NCH>([&](auto S) { signs[S] = sign_bits8<8 * S>(x, xval); });
     } else {
-        static_for<0, 2>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
+        static_for<0, NCH>([&](auto S) { signs[S] = parity_fold8<8 * S>(x, w, xval); });
     }
     float gmax = xval[0];
 #pragma unroll
-    for (int i = 1; i < 16; i++) gmax = fmaxf(gmax, xval[i]);
-    gmax = fmaxf(gmax, __shfl_xor(gmax, 1));
+    for (int i = 1; i < VPL; i++) gmax = fmaxf(gmax, xval[i]);
+#pragma unroll
+    for (int m = 1; m < LPG; m <<= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, m));
     const bool active = IS_S ? gmax > 0 : gmax >= 1e-8f;
     const float gsafe = active ? gmax : 1.0f;
     float scale = gmax / 15.0f, best = 0.0f;
-    int Wg[4];
-    bool og[4];
+    int Wg[NSL];
+    bool og[NSL];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < NSL; k++) {
         Wg[k] = 0;
         og[k] = !IS_S;
     }
-    // the group's two sums: this lane's half-tree joined with the partner's
-    auto group_sums = [&](const int (&gi)[4], float& sumqx, float& sumq2) {
+    auto group_sums = [&](const int (&gi)[NSL], float& sumqx, float& sumq2) {
         float hx, h2;
-        iq_tree_sums<3, 4, 4>(glds, gi, w, xval, hx, h2);
-        sumqx = hx + __shfl_xor(hx, 1);
-        sumq2 = h2 + __shfl_xor(h2, 1);
+        iq_tree_sums<3, 4, NSL>(glds, gi, w, xval, hx, h2);
+#pragma unroll
+        for (int m = 1; m < LPG; m <<= 1) {
+            hx = hx + __shfl_xor(hx, m);
+            h2 = h2 + __shfl_xor(h2, m);
+        }
+        sumqx = hx;
+        sumq2 = h2;
     };
     wave_sync();   // glds ready
 #pragma unroll 1
     for (int st = 0; st < steps.n; st++) {
         const float inv = rdiv(steps.v[st], gsafe), sc = 1.0f / inv;
-        int gi[4];
-        bool on[4];
-        uint32_t ci[4];
-        iq_codes<3, 4, 4>(T, xval, inv, ci);
-        static_for<0, 4>([&](auto S) {
+        int gi[NSL];
+        bool on[NSL];
+        uint32_t ci[NSL];
+        iq_codes<3, 4, NSL>(T, xval, inv, ci);
+        static_for<0, NSL>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
         float sumqx, sumq2;
@@ -744,32 +753,30 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
             scale = ns;
             best = ns * sumqx;
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
+            for (int k = 0; k < NSL; k++) {
                 Wg[k] = gi[k];
                 og[k] = on[k];
             }
         }
     }
-    bool anyoff = false;
+    int anyoff = 0;
 #pragma unroll
-    for (int k = 0; k < 4; k++) anyoff = anyoff || !og[k];
-    // the exchange runs in every lane (behind `||` it would run only where
-    // anyoff is false and read inactive partners)
-    const int partner_off = __shfl_xor((int)anyoff, 1);
-    anyoff = anyoff || partner_off != 0;
+    for (int k = 0; k < NSL; k++) anyoff |= og[k] ? 0 : 1;
+#pragma unroll
+    for (int m = 1; m < LPG; m <<= 1) anyoff |= __shfl_xor(anyoff, m);
     const bool redo = active && anyoff && scale > 0;
     {
         const float inv2 = 1.0f / (redo ? scale : 1.0f);
-        int w2[4];
-        bool on[4];
-        uint32_t ci[4];
-        iq_codes<3, 4, 4>(T, xval, inv2, ci);
-        static_for<0, 4>([&](auto S) {
+        int w2[NSL];
+        bool on[NSL];
+        uint32_t ci[NSL];
+        iq_codes<3, 4, NSL>(T, xval, inv2, ci);
+        static_for<0, NSL>([&](auto S) {
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);
         });
 #pragma unroll
-        for (int k = 0; k < 4; k++)
+        for (int k = 0; k < NSL; k++)
             if (redo && (IS_S || !og[k])) Wg[k] = w2[k];
         float sumqx, sumq2;
         group_sums(Wg, sumqx, sumq2);
@@ -778,9 +785,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
     if (active && scale < 0) {
         scale = -scale;
 #pragma unroll
-        for (int k = 0; k < 2; k++) signs[k] = (~signs[k]) & SMASK;
+        for (int k = 0; k < NCH; k++) signs[k] = (~signs[k]) & SMASK;
     }
-    if (half == 0) {
+    if (q == 0) {
         s.sc[slot][grp] = active ? scale : 0.0f;
         act_lds[slot][grp] = active ? 1 : 0;
     }
@@ -797,17 +804,18 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
             o[0] = (uint8_t)h;
             o[1] = (uint8_t)(h >> 8);
         }
-        // sign word of the group: 7 bits per 8-value chunk, chunks 2h, 2h+1 here
-        uint32_t part = 0;
+        uint32_t word = 0;
 #pragma unroll
-        for (int k = 0; k < 2; k++) part |= (uint32_t)(active ? signs[k] : 0) << (7 * (2 * half + k));
-        uint32_t word = part | (uint32_t)__shfl_xor((int)part, 1);
+        for (int k = 0; k < NCH; k++) word |= (uint32_t)(active ? signs[k] : 0) << (7 * (NCH * q + k));
+#pragma unroll
+        for (int m = 1; m < LPG; m <<= 1) word |= (uint32_t)__shfl_xor((int)word, m);
         word |= (uint32_t)l[grp] << 28;
         if (!has) word = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) o[2 + 8 * grp + 4 * half + k] = (uint8_t)((has && active) ? Wg[k] : 0);
+        for (int k = 0; k < NSL; k++) o[2 + 8 * grp + NSL * q + k] = (uint8_t)((has && active) ? Wg[k] : 0);
+        constexpr int WB = 4 / LPG;
 #pragma unroll
-        for (int k = 0; k < 2; k++) o[66 + 4 * grp + 2 * half + k] = (uint8_t)(word >> (8 * (2 * half + k)));
+        for (int k = 0; k < WB; k++) o[66 + 4 * grp + WB * q + k] = (uint8_t)(word >> (8 * (WB * q + k)));
     } else {
         if (p.g == 0) {
             const uint32_t h = f16_bits(has ? d * 1.033f : 0.0f);
@@ -816,16 +824,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(4))) void k_
         }
         int hb = 0;
 #pragma unroll
-        for (int k = 0; k < 4; k++) hb |= (Wg[k] >> 8) << (4 * half + k);
-        hb |= __shfl_xor(hb, 1);
-        if (half == 0) o[66 + grp] = (uint8_t)(active ? hb : 0);
+        for (int k = 0; k < NSL; k++) hb |= (Wg[k] >> 8) << (NSL * q + k);
+#pragma unroll
+        for (int m = 1; m < LPG; m <<= 1) hb |= __shfl_xor(hb, m);
+        if (q == 0) o[66 + grp] = (uint8_t)(active ? hb : 0);
         if (active) {
             int slot_idx = 0;                  // live groups compact to the front (iq3_s.py:113-122)
             for (int j = 0; j < grp; j++) slot_idx += act_lds[slot][j];
 #pragma unroll
-            for (int k = 0; k < 4; k++) o[2 + 8 * slot_idx + 4 * half + k] = (uint8_t)(Wg[k] & 255);
+            for (int k = 0; k < NSL; k++) o[2 + 8 * slot_idx + NSL * q + k] = (uint8_t)(Wg[k] & 255);
 #pragma unroll
-            for (int k = 0; k < 2; k++) o[74 + 4 * slot_idx + 2 * half + k] = (uint8_t)signs[k];
+            for (int k = 0; k < NCH; k++) o[74 + 4 * slot_idx + NCH * q + k] = (uint8_t)signs[k];
         }
         if (p.g < 4) o[106 + p.g] = (uint8_t)(has ? (l[2 * p.g] | (l[2 * p.g + 1] << 4)) : 0);
     }

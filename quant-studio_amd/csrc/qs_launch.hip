@@ -141,14 +141,18 @@ hipError_t launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
     case QS_TYPE_IQ2_S:
         return launch(k_iq2_xs_s<SRC, true, SQ>, sb4, wave, st, a, tabs[IQT_G2_1024],
                       iq_steps(5.0f, 0.1f, -9, 9));
-    case QS_TYPE_IQ3_XXS:     // _STEPS iq3_xxs.py:22
-        return launch(k_iq3<SRC, false, true, SQ>, sb4, wave, st, a, tabs[IQT_G3_256],
+    case QS_TYPE_IQ3_XXS: {    // _STEPS iq3_xxs.py:22
+        const dim3 sb2((unsigned)((a.n_units + 1) / 2));
+        return launch(k_iq3<SRC, false, true, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_256],
                       iq_steps(15.0f, 0.2f, -15, 15));
-    case QS_TYPE_IQ3_S:       // _STEPS iq3_s.py:22
-        return imat ? launch(k_iq3<SRC, true, true, SQ>, sb4, wave, st, a, tabs[IQT_G3_512],
+    }
+    case QS_TYPE_IQ3_S: {      // _STEPS iq3_s.py:22
+        const dim3 sb2((unsigned)((a.n_units + 1) / 2));
+        return imat ? launch(k_iq3<SRC, true, true, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_512],
                              iq_steps(15.0f, 0.2f, -9, 9))
-                    : launch(k_iq3<SRC, true, false, SQ>, sb4, wave, st, a, tabs[IQT_G3_512],
+                    : launch(k_iq3<SRC, true, false, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_512],
                              iq_steps(15.0f, 0.2f, -9, 9));
+    }
     default:
         return hipErrorInvalidValue;
     }
