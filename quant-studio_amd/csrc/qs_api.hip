@@ -12,6 +12,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <utility>
 #include <vector>
@@ -126,7 +127,10 @@ struct HostTab {
 // kmap plus, for every off-grid code the level projection can produce (IQ2:
 // levels 0..2, IQ3: 0..7), the grid points within its nwant smallest distinct
 // squared distances in (distance, index) order -- the neighbour tables of
-// iq2.py:31-74, iq2xs_common.py:41-95, iq3_common.py:29-68.
+// iq2.py:31-74, iq2xs_common.py:41-95, iq3_common.py:29-68. The codes are
+// split over host threads in contiguous ranges; each range's lists are
+// appended in code order and the ranges joined in order, so the tables are
+// the sequential build's byte for byte.
 HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch, int maxch) {
     const int nsub = bits == 2 ? 8 : 4, lmask = (1 << bits) - 1, lmax = bits == 2 ? 2 : 7;
     const int ksize = bits == 2 ? 43692 : 4096;
@@ -139,42 +143,71 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
         t.cinfo[grid[i]] = qs::CI_ON_GRID | (uint32_t)i;
     }
     t.code0 = kmap[0] >= 0 ? kmap[0] : 0;
-    std::vector<int> gl(gs * nsub), d2(gs);
+    std::vector<int> gl(gs * nsub);
     for (int i = 0; i < gs; i++)
         for (int j = 0; j < nsub; j++) gl[i * nsub + j] = 2 * ((grid[i] >> (bits * j)) & lmask) + 1;
-    for (int c = 0; c < ksize; c++) {
-        if (kmap[c] >= 0) continue;
-        int p[8];
+    // lists of codes [c0, c1): cinfo entries with starts relative to the range
+    struct Part {
+        std::vector<uint16_t> nbr;
         bool ok = true;
-        for (int j = 0; j < nsub; j++) {
-            const int l = (c >> (bits * j)) & lmask;
-            ok = ok && l <= lmax;
-            p[j] = 2 * l + 1;
+    };
+    auto build_range = [&](int c0, int c1, Part& part) {
+        std::vector<int> d2(gs);
+        for (int c = c0; c < c1; c++) {
+            if (kmap[c] >= 0) continue;
+            int p[8];
+            bool ok = true;
+            for (int j = 0; j < nsub; j++) {
+                const int l = (c >> (bits * j)) & lmask;
+                ok = ok && l <= lmax;
+                p[j] = 2 * l + 1;
+            }
+            if (!ok) continue;
+            // the nwant smallest distinct distances (ascending), then every grid
+            // point within the largest of them, in (distance, index) order
+            int small[4];
+            int nd = 0;
+            for (int i = 0; i < gs; i++) {
+                int v = 0;
+                for (int j = 0; j < nsub; j++) v += (p[j] - gl[i * nsub + j]) * (p[j] - gl[i * nsub + j]);
+                d2[i] = v;
+                int pos = 0;
+                while (pos < nd && small[pos] < v) pos++;
+                if ((pos < nd && small[pos] == v) || pos >= nwant) continue;
+                for (int q = std::min(nd, nwant - 1); q > pos; q--) small[q] = small[q - 1];
+                small[pos] = v;
+                nd = std::min(nd + 1, nwant);
+            }
+            const size_t start = part.nbr.size();     // a multiple of ch: one aligned vector per chunk
+            for (int r = 0; r < nd; r++)
+                for (int i = 0; i < gs; i++)
+                    if (d2[i] == small[r]) part.nbr.push_back((uint16_t)i);
+            const size_t len = part.nbr.size() - start;
+            part.nbr.resize((part.nbr.size() + ch - 1) / ch * ch, 0);
+            t.cinfo[c] = (uint32_t)((start / ch) << 12) | (uint32_t)len;
+            part.ok = part.ok && len < 4096 && len <= (size_t)ch * maxch;
         }
-        if (!ok) continue;
-        // the nwant smallest distinct distances (ascending), then every grid
-        // point within the largest of them, in (distance, index) order
-        int small[4];
-        int nd = 0;
-        for (int i = 0; i < gs; i++) {
-            int v = 0;
-            for (int j = 0; j < nsub; j++) v += (p[j] - gl[i * nsub + j]) * (p[j] - gl[i * nsub + j]);
-            d2[i] = v;
-            int pos = 0;
-            while (pos < nd && small[pos] < v) pos++;
-            if ((pos < nd && small[pos] == v) || pos >= nwant) continue;
-            for (int q = std::min(nd, nwant - 1); q > pos; q--) small[q] = small[q - 1];
-            small[pos] = v;
-            nd = std::min(nd + 1, nwant);
+    };
+    const int nthr = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<Part> parts(nthr);
+    std::vector<std::thread> threads;
+    for (int k = 0; k < nthr; k++)
+        threads.emplace_back(build_range, (int)((int64_t)ksize * k / nthr), (int)((int64_t)ksize * (k + 1) / nthr),
+                             std::ref(parts[k]));
+    for (auto& th : threads) th.join();
+    // join the ranges in code order, moving each range's starts by the lists before it
+    size_t base = 0;
+    for (int k = 0; k < nthr; k++) {
+        const int c0 = (int)((int64_t)ksize * k / nthr), c1 = (int)((int64_t)ksize * (k + 1) / nthr);
+        for (int c = c0; c < c1; c++) {
+            if (kmap[c] >= 0 || !(t.cinfo[c] & 0xfffu)) continue;
+            const size_t start = ((t.cinfo[c] >> 12) & 0x7ffffu) + base / ch;
+            t.ok = t.ok && start < (1u << 19);
+            t.cinfo[c] = (uint32_t)(start << 12) | (t.cinfo[c] & 0xfffu);
         }
-        const size_t start = t.nbr.size();     // a multiple of ch: one aligned vector per chunk
-        for (int r = 0; r < nd; r++)
-            for (int i = 0; i < gs; i++)
-                if (d2[i] == small[r]) t.nbr.push_back((uint16_t)i);
-        const size_t len = t.nbr.size() - start;
-        t.nbr.resize((t.nbr.size() + ch - 1) / ch * ch, 0);
-        t.cinfo[c] = (uint32_t)((start / ch) << 12) | (uint32_t)len;
-        t.ok = t.ok && len < 4096 && start / ch < (1u << 19) && len <= (size_t)ch * maxch;
+        t.nbr.insert(t.nbr.end(), parts[k].nbr.begin(), parts[k].nbr.end());
+        base += parts[k].nbr.size();
+        t.ok = t.ok && parts[k].ok;
     }
     return t;
 }
@@ -221,19 +254,29 @@ struct DevTables {
     std::array<const uint32_t*, SQM_N> sqrt{};
 };
 
-// the three maps, expanded on the host once per process (false if the
-// embedded AMD map is corrupt)
-bool sqrt_map_bits(std::array<std::vector<uint32_t>, SQM_N>*& out) {
-    static std::once_flag once;
+// one map's bits, expanded on the host once per process: the Intel set from
+// its key gaps, the AMD pair from the embedded 2-bit map only when an AMD
+// mode first runs (false if that map is corrupt)
+bool sqrt_map_bits(int id, const std::vector<uint32_t>*& out) {
+    static std::once_flag intel_once, amd_once;
     static std::array<std::vector<uint32_t>, SQM_N> bits;
-    static bool ok = false;
-    std::call_once(once, [] {
-        for (auto& b : bits) b.assign(1u << 19, 0u);
-        uint32_t key = 0;
-        for (int i = 0; i < QS_SQRT_DOWN_N; i++) {
-            key += QS_SQRT_DOWN_GAPS[i];
-            bits[SQM_INTEL_DOWN][key >> 5] |= 1u << (key & 31u);
-        }
+    static bool amd_ok = false;
+    out = &bits[id];
+    if (id == SQM_INTEL_DOWN) {
+        std::call_once(intel_once, [] {
+            auto& b = bits[SQM_INTEL_DOWN];
+            b.assign(1u << 19, 0u);
+            uint32_t key = 0;
+            for (int i = 0; i < QS_SQRT_DOWN_N; i++) {
+                key += QS_SQRT_DOWN_GAPS[i];
+                b[key >> 5] |= 1u << (key & 31u);
+            }
+        });
+        return true;
+    }
+    std::call_once(amd_once, [] {
+        bits[SQM_AMD_DOWN].assign(1u << 19, 0u);
+        bits[SQM_AMD_UP].assign(1u << 19, 0u);
         std::vector<unsigned char> packed(1u << 22);
         uLongf len = (uLongf)packed.size();
         const uLong clen = (uLong)(qs_sqrt_amd_blob_end - qs_sqrt_amd_blob);
@@ -244,10 +287,9 @@ bool sqrt_map_bits(std::array<std::vector<uint32_t>, SQM_N>*& out) {
             if (code == 3) return;
             if (code) bits[code == 1 ? SQM_AMD_DOWN : SQM_AMD_UP][k >> 5] |= 1u << (k & 31u);
         }
-        ok = true;
+        amd_ok = true;
     });
-    out = &bits;
-    return ok;
+    return amd_ok;
 }
 
 template <typename T>
@@ -279,9 +321,9 @@ bool device_tables_locked(int dev, int iq_table, const std::array<bool, SQM_N>& 
     DevTables& d = g_dev_state[dev];
     for (int m = 0; m < SQM_N; m++) {
         if (!maps[m] || d.sqrt[m]) continue;
-        std::array<std::vector<uint32_t>, SQM_N>* bits = nullptr;
-        if (!sqrt_map_bits(bits)) return false;
-        d.sqrt[m] = upload((*bits)[m]);
+        const std::vector<uint32_t>* bits = nullptr;
+        if (!sqrt_map_bits(m, bits)) return false;
+        d.sqrt[m] = upload(*bits);
         if (!d.sqrt[m]) return false;
     }
     if (iq_table >= 0 && !d.iq[iq_table].grid) {
