@@ -26,7 +26,8 @@ struct QkxResult {
 };
 
 // make_qkx_quants_eager kq_common.py:51-96 for one group of N values.
-template <int N, bool MAD>
+// SPEC: divide the next candidate's inverse scale during the error pass (below).
+template <int N, bool MAD, bool SPEC = false>
 QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& steps, float fmax) {
     float mn = x[0], mx = x[0];
 #pragma unroll
@@ -58,15 +59,30 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
 
     // 16-value groups load each step one candidate ahead, so the scalar
     // load's latency is not waited for at the top of every candidate (Q2_K
-    // 2-6% faster); the 32-value loop measured 0-1.4% slower that way
+    // 2-6% faster). With SPEC the next candidate's inverse scale is divided
+    // both ways while this candidate's error pass runs, for a kept min
+    // (mx - mn) and for this candidate's min should it be accepted
+    // (mx - this_min), so no division heads the next candidate; the quotients
+    // are the ones dividing after the accept gives. Q4_K / Q5_K with imatrix
+    // (37 candidates) run 1.4-1.9% faster that way; without imatrix they ran
+    // 1.4-2.3% slower and 16-value groups 5-9% slower (one more division per
+    // candidate weighs more there), so only the former use it.
+    static_assert(!SPEC || N == 32, "SPEC is timed for 32-value groups only");
     constexpr bool AHEAD = N == 16;
     float step_next = steps.v[0];
+    float isc_keep = SPEC ? step_next / den : 0.0f, isc_acc = isc_keep;
+    bool accepted = false;
 #pragma unroll 1
     for (int s = 0; s < steps.n; s++) {
-        const float step = AHEAD ? step_next : steps.v[s];
-        if constexpr (AHEAD) step_next = steps.v[s + 1 < 40 ? s + 1 : 39];
-        den = degen ? 1.0f : mx - mn;
-        const float isc = step / den;
+        float isc;
+        if constexpr (SPEC) {
+            isc = accepted ? isc_acc : isc_keep;
+        } else {
+            const float step = AHEAD ? step_next : steps.v[s];
+            if constexpr (AHEAD) step_next = steps.v[s + 1 < 40 ? s + 1 : 39];
+            den = degen ? 1.0f : mx - mn;
+            isc = step / den;
+        }
         // the three tree sums are formed 8 values at a time (the tree over N
         // is the trees over its 8-value blocks, then the tree over the block
         // sums), so only one block of products is live at once
@@ -96,6 +112,12 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
             this_scale = sum_xl / fmaxf(sum_l2, F32_TINY);
             this_min = 0.0f;
         }
+        float next_keep = 0.0f, next_acc = 0.0f;
+        if constexpr (SPEC) {
+            const float step = steps.v[s + 1 < 40 ? s + 1 : 39];
+            next_keep = step / (degen ? 1.0f : mx - mn);
+            next_acc = step / (degen ? 1.0f : mx - this_min);
+        }
         float se[NB];
 #pragma unroll
         for (int k = 0; k < NB; k++) {
@@ -111,7 +133,10 @@ QS_DEV QkxResult qkx_fit(const float (&x)[N], const float (&w)[N], const Steps& 
             se[k] = tree_sum(e8);
         }
         const float cur = tree_sum(se);
-        if (D > 0 && cur < best && !degen) {
+        accepted = D > 0 && cur < best && !degen;
+        isc_keep = next_keep;
+        isc_acc = next_acc;
+        if (accepted) {
             best_isc = isc;
             best_mn = mn;
             scale = this_scale;

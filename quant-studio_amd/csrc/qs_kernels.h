@@ -339,7 +339,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4
         for (int i = 0; i < 32; i++) w[i] = av + fabsf(x[i]);
     }
 
-    const QkxResult r = qkx_fit<32, false>(x, w, steps, FMAX);
+    const QkxResult r = qkx_fit<32, false, IMAT>(x, w, steps, FMAX);
     s.sc[slot][g] = r.scale;
     s.mn[slot][g] = r.the_min;
     if constexpr (IMAT) s.sw[slot][g] = cascade8_sum(w);
