@@ -102,8 +102,12 @@ int qs_get_sqrt_rounding(void);
  * quant-studio.py:396-399). */
 int qs_type_supported(int ggml_type);
 
-/* 1 if the type cannot run without an imatrix (QuantSpec.needs_imatrix,
- * kernels/common.py:33), 0 if not, QS_ENOTSUP for an unknown type. */
+/* 1 if the type's QuantSpec.needs_imatrix is set (kernels/common.py:33): the
+ * command line refuses to plan it without an imatrix (quant-studio.py:400-406).
+ * 0 if not, QS_ENOTSUP for an unknown type. qs_quantize() itself requires an
+ * imatrix only for IQ2_XXS, IQ2_XS and IQ2_S, whose reference quantizers have
+ * no path without one; IQ3_XXS (needs_imatrix = 1) quantizes without one as
+ * quantize_iq3_xxs(x, None) does (weights x^2, iq3_xxs.py:41-42). */
 int qs_type_needs_imatrix(int ggml_type);
 
 /* 1 if the type uses an imatrix when one is given (QuantSpec.uses_imatrix,
@@ -119,7 +123,8 @@ int64_t qs_row_bytes(int ggml_type, int64_t k);
  *   src:           device pointer to the first row; 16-byte aligned
  *   src_row_stride_bytes: distance between rows, a multiple of 16, >= k*elem
  *   imatrix:       device pointer to k f32 column weights, or NULL; required
- *                  when qs_type_needs_imatrix(); ignored by Q4_0
+ *                  by IQ2_XXS / IQ2_XS / IQ2_S (QS_EINVAL otherwise); ignored
+ *                  by Q4_0, Q4_1, Q5_0, Q5_1 and Q8_0
  *   dst:           device pointer receiving n_rows * qs_row_bytes(k) bytes;
  *                  dst_bytes must be at least that
  *   hip_stream:    hipStream_t to launch on (NULL = null stream)

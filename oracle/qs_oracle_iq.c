@@ -505,7 +505,8 @@ int qs_oracle_iq(int type, const float *x, const float *qw, uint8_t *out) {
     case QSO_IQ2_XXS: if (!qw) return 1; iq2_xxs_block(x, qw, out); return 0;
     case QSO_IQ2_XS: if (!qw) return 1; iq2_xs_s_block(x, qw, out, 0); return 0;
     case QSO_IQ2_S: if (!qw) return 1; iq2_xs_s_block(x, qw, out, 1); return 0;
-    case QSO_IQ3_XXS: if (!qw) return 1; iq3_block(x, qw, out, 0); return 0;
+    /* quantize_iq3_xxs takes qw = None: weights x^2 (iq3_xxs.py:41-42) */
+    case QSO_IQ3_XXS: iq3_block(x, qw, out, 0); return 0;
     case QSO_IQ3_S: iq3_block(x, qw, out, 1); return 0;
     default: return 1;
     }

@@ -76,6 +76,11 @@ struct TypeInfo {
     const char* name;
     int blk, bytes;
     bool needs_imatrix, uses_imatrix;
+    // the reference's quantizer function has no path without an imatrix
+    // (IQ2_XXS / IQ2_XS / IQ2_S: iq2.py:418-431, iq2_xs.py:20-29, iq2_s.py:21-30
+    // index qw unconditionally); IQ3_XXS's needs_imatrix is the command line's
+    // policy only, its function takes None (iq3_xxs.py:41-42)
+    bool fn_requires_imatrix;
 };
 
 // block sizes and type sizes: BLOCK_BYTES of each reference module
@@ -83,26 +88,26 @@ struct TypeInfo {
 // q6_k.py:19, iq4_xs.py:20, iq2.py:27, ...); imatrix flags from the SPECS
 // entries (q4_0.py:40-43, q2_k.py:88-91, ..., iq3_s.py:148-151).
 constexpr TypeInfo kTypes[] = {
-    {QS_TYPE_Q4_0, "q4_0", 32, 18, false, false},
-    {QS_TYPE_Q2_K, "q2_k", 256, 84, false, true},
-    {QS_TYPE_Q3_K, "q3_k", 256, 110, false, true},
-    {QS_TYPE_Q4_K, "q4_k", 256, 144, false, true},
-    {QS_TYPE_Q5_K, "q5_k", 256, 176, false, true},
-    {QS_TYPE_Q6_K, "q6_k", 256, 210, false, true},
-    {QS_TYPE_IQ4_XS, "iq4_xs", 256, 136, false, true},
-    {QS_TYPE_IQ2_XXS, "iq2_xxs", 256, 66, true, true},
-    {QS_TYPE_IQ2_XS, "iq2_xs", 256, 74, true, true},
-    {QS_TYPE_IQ2_S, "iq2_s", 256, 82, true, true},
-    {QS_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, true, true},
-    {QS_TYPE_IQ3_S, "iq3_s", 256, 110, false, true},
+    {QS_TYPE_Q4_0, "q4_0", 32, 18, false, false, false},
+    {QS_TYPE_Q2_K, "q2_k", 256, 84, false, true, false},
+    {QS_TYPE_Q3_K, "q3_k", 256, 110, false, true, false},
+    {QS_TYPE_Q4_K, "q4_k", 256, 144, false, true, false},
+    {QS_TYPE_Q5_K, "q5_k", 256, 176, false, true, false},
+    {QS_TYPE_Q6_K, "q6_k", 256, 210, false, true, false},
+    {QS_TYPE_IQ4_XS, "iq4_xs", 256, 136, false, true, false},
+    {QS_TYPE_IQ2_XXS, "iq2_xxs", 256, 66, true, true, true},
+    {QS_TYPE_IQ2_XS, "iq2_xs", 256, 74, true, true, true},
+    {QS_TYPE_IQ2_S, "iq2_s", 256, 82, true, true, true},
+    {QS_TYPE_IQ3_XXS, "iq3_xxs", 256, 98, true, true, false},
+    {QS_TYPE_IQ3_S, "iq3_s", 256, 110, false, true, false},
     // ggml formats without a reference module (quant-studio.py:396-399 stops
     // on them): block layouts from the GGUF format; the imatrix is used by
     // IQ4_NL only (the 32-value integer formats ignore it, as Q4_0 does)
-    {QS_TYPE_Q4_1, "q4_1", 32, 20, false, false},
-    {QS_TYPE_Q5_0, "q5_0", 32, 22, false, false},
-    {QS_TYPE_Q5_1, "q5_1", 32, 24, false, false},
-    {QS_TYPE_Q8_0, "q8_0", 32, 34, false, false},
-    {QS_TYPE_IQ4_NL, "iq4_nl", 32, 18, false, true},
+    {QS_TYPE_Q4_1, "q4_1", 32, 20, false, false, false},
+    {QS_TYPE_Q5_0, "q5_0", 32, 22, false, false, false},
+    {QS_TYPE_Q5_1, "q5_1", 32, 24, false, false, false},
+    {QS_TYPE_Q8_0, "q8_0", 32, 34, false, false, false},
+    {QS_TYPE_IQ4_NL, "iq4_nl", 32, 18, false, true, false},
 };
 
 const TypeInfo* find_type(int id) {
@@ -112,6 +117,15 @@ const TypeInfo* find_type(int id) {
 }
 
 bool has_kernel(int id) { return find_type(id) != nullptr; }
+
+}  // namespace
+
+bool qs_host::quantizer_requires_imatrix(int ggml_type) {
+    const TypeInfo* t = find_type(ggml_type);
+    return t && t->fn_requires_imatrix;
+}
+
+namespace {
 
 // ---- IQ grid tables: built once per process, uploaded once per device ----
 
@@ -428,7 +442,7 @@ int qs_quantize(int ggml_type, int src_type, const void* src, int64_t n_rows, in
     if (dst_bytes < n_rows * rb)
         return fail(QS_EINVAL, "dst holds %lld bytes, %lld needed", (long long)dst_bytes,
                     (long long)(n_rows * rb));
-    if (t->needs_imatrix && !imatrix) return fail(QS_EINVAL, "%s requires an imatrix", t->name);
+    if (t->fn_requires_imatrix && !imatrix) return fail(QS_EINVAL, "%s requires an imatrix", t->name);
     const bool imat = t->uses_imatrix && imatrix != nullptr;
 
     qs::KArgs a;

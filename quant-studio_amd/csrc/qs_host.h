@@ -10,4 +10,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Clear the calling thread's message.
 void clear_error();
 
+// True for the types whose quantizer cannot run without an imatrix
+// (IQ2_XXS / IQ2_XS / IQ2_S); every other type runs with imatrix == NULL.
+bool quantizer_requires_imatrix(int ggml_type);
+
 }  // namespace qs_host

@@ -143,8 +143,10 @@ hipError_t launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
                       iq_steps(5.0f, 0.1f, -9, 9));
     case QS_TYPE_IQ3_XXS: {    // _STEPS iq3_xxs.py:22
         const dim3 sb2((unsigned)((a.n_units + 1) / 2));
-        return launch(k_iq3<SRC, false, true, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_256],
-                      iq_steps(15.0f, 0.2f, -15, 15));
+        return imat ? launch(k_iq3<SRC, false, true, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_256],
+                             iq_steps(15.0f, 0.2f, -15, 15))
+                    : launch(k_iq3<SRC, false, false, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_256],
+                             iq_steps(15.0f, 0.2f, -15, 15));
     }
     case QS_TYPE_IQ3_S: {      // _STEPS iq3_s.py:22
         const dim3 sb2((unsigned)((a.n_units + 1) / 2));

@@ -321,7 +321,7 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
                     (long long)k);
     if (n_rows == 0) return 0;
     if (!src) return fail(QS_EINVAL, "null src");
-    if (qs_type_needs_imatrix(ggml_type) == 1 && !imatrix)
+    if (qs_host::quantizer_requires_imatrix(ggml_type) && !imatrix)
         return fail(QS_EINVAL, "ggml type %d requires an imatrix", ggml_type);
     const bool use_qw = imatrix && qs_type_uses_imatrix(ggml_type) == 1;
     hipError_t e = hipSetDevice(p->device);

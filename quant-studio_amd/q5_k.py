@@ -1,0 +1,15 @@
+"""Q5_K: the reference module's quantizer and SPECS entry (kernels/q5_k.py:25,
+:89-92), computed by the HIP kernel k_q45_k through the C ABI."""
+
+from . import ALL_SPECS, quantize
+
+
+def quantize_q5_k(x, qw):
+    """x: (n_rows, k) float32 / float16 / bfloat16 on a ROCm device or the CPU,
+    k % 256 == 0; qw: (k,) float32 imatrix weights on x's device, or None.
+    Returns (n_rows, k//256 * 176) uint8 on x's device (a CPU x is staged
+    through the current ROCm device)."""
+    return quantize(int(ALL_SPECS['q5_k'].ggml_type), x, qw)
+
+
+SPECS = {'q5_k': ALL_SPECS['q5_k']}

@@ -13,7 +13,7 @@ kernels/q4_0.py:6-7, ...). gguf-py is not installed here, so this script
 provides a minimal stand-in module exposing those names with the public GGUF
 enum values; no arithmetic depends on it.
 
-Usage: python tests/golden/gen_golden.py [--ref /root/reference]
+Usage: python tests/golden/gen_golden.py [--ref /root/reference] [--only TYPE ...]
 """
 
 from __future__ import annotations
@@ -69,7 +69,9 @@ TYPES = [
     ("iq2_xxs", "iq2", "quantize_iq2_xxs", ("imat",)),
     ("iq2_xs", "iq2_xs", "quantize_iq2_xs", ("imat",)),
     ("iq2_s", "iq2_s", "quantize_iq2_s", ("imat",)),
-    ("iq3_xxs", "iq3_xxs", "quantize_iq3_xxs", ("imat",)),
+    # the function takes None (weights x^2, iq3_xxs.py:41-42) although the
+    # type's QuantSpec requires an imatrix (the command line refuses it)
+    ("iq3_xxs", "iq3_xxs", "quantize_iq3_xxs", ("none", "imat")),
     ("iq3_s", "iq3_s", "quantize_iq3_s", ("none", "imat")),
 ]
 
@@ -146,6 +148,7 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--out", default=str(HERE))
+    ap.add_argument("--only", nargs="*", help="write only these types' files (inputs.npz is left as is)")
     args = ap.parse_args()
 
     install_enum_module()
@@ -158,7 +161,8 @@ def main() -> None:
     for cname, c in cases.items():
         inputs[f"{cname}.x"] = c["x"]
         inputs[f"{cname}.imat"] = c["imat"]
-    np.savez_compressed(Path(args.out) / "inputs.npz", **inputs)
+    if not args.only:
+        np.savez_compressed(Path(args.out) / "inputs.npz", **inputs)
 
     # per-group results of the shared IQ2_XS / IQ2_S search (iq2xs_common.scale_search),
     # recorded by wrapping the function the quantizers call
@@ -189,6 +193,8 @@ def main() -> None:
     xs_common.search_codes = recording_search
 
     for tname, mod, fn, modes in TYPES:
+        if args.only and tname not in args.only:
+            continue
         m = importlib.import_module(f"kernels.{mod}")
         f = getattr(m, fn)
         if tname in ("iq2_xs", "iq2_s"):

@@ -57,6 +57,35 @@ def test_type_flags_match_reference_specs(qs):
     assert L.qs_type_needs_imatrix(99) == -95
 
 
+# the reference's per-type modules: module -> (function, its parameters)
+# (kernels/q4_0.py:14, q2_k.py:25, q3_k.py:23, q4_k.py:25, q5_k.py:25,
+# q6_k.py:22, iq4_xs.py:149, iq2.py:418, iq2_xs.py:20, iq2_s.py:21,
+# iq3_xxs.py:31, iq3_s.py:31), each with a SPECS dict of its type
+REFERENCE_MODULES = {
+    "q4_0": ("quantize_q4_0", ["x"]), "q2_k": ("quantize_q2_k", ["x", "qw"]),
+    "q3_k": ("quantize_q3_k", ["x", "qw"]), "q4_k": ("quantize_q4_k", ["x", "qw"]),
+    "q5_k": ("quantize_q5_k", ["x", "qw"]), "q6_k": ("quantize_q6_k", ["x", "qw"]),
+    "iq4_xs": ("quantize_iq4_xs", ["x", "qw"]), "iq2": ("quantize_iq2_xxs", ["x", "qw", "T"]),
+    "iq2_xs": ("quantize_iq2_xs", ["x", "qw"]), "iq2_s": ("quantize_iq2_s", ["x", "qw"]),
+    "iq3_xxs": ("quantize_iq3_xxs", ["x", "qw"]), "iq3_s": ("quantize_iq3_s", ["x", "qw"]),
+}
+
+
+def test_per_type_modules_mirror_the_reference(qs):
+    """`kernels.<module>.quantize_<type>` callers (tools/dev_gpu_check.py:22-24)
+    find the same module, function and parameter names, and each module's
+    SPECS holds its registry entry; the five extra types follow the pattern."""
+    import importlib
+    import inspect
+    extra = {t: (f"quantize_{t}", ["x", "qw"]) for t in ("q4_1", "q5_0", "q5_1", "q8_0", "iq4_nl")}
+    for mod, (fn, params) in {**REFERENCE_MODULES, **extra}.items():
+        m = importlib.import_module(f"quant-studio_amd.{mod}")
+        f = getattr(m, fn)
+        assert list(inspect.signature(f).parameters) == params, mod
+        (name, spec), = m.SPECS.items()
+        assert fn == f"quantize_{name}" and spec is qs.ALL_SPECS[name], mod
+
+
 def test_registry_lists_only_types_with_kernels(qs):
     L = qs.library()
     for name, spec in qs.ALL_SPECS.items():
@@ -91,12 +120,22 @@ def test_quantize_rejects_bad_arguments_before_launch(qs):
     assert _call(L, 12, n=(1 << 34) // 256 + 1, k=256, stride=512) == -22
 
 
-def test_needs_imatrix_types_reject_missing_imatrix(qs):
+def test_iq2_types_reject_missing_imatrix(qs):
+    """IQ2_XXS / IQ2_XS / IQ2_S refuse a NULL imatrix before any device work
+    (their reference quantizers index qw unconditionally, iq2.py:418-431,
+    iq2_xs.py:20-29, iq2_s.py:21-30). IQ3_XXS, whose QuantSpec also has
+    needs_imatrix (a command-line policy), goes on without one as
+    quantize_iq3_xxs(x, None) does (iq3_xxs.py:41-42): with no device here it
+    fails later, at the table upload, not at the imatrix check."""
     L = qs.library()
-    for name, spec in qs.ALL_SPECS.items():
-        if spec.needs_imatrix and L.qs_type_supported(int(spec.ggml_type)):
-            assert _call(L, int(spec.ggml_type)) == -22
-            assert b"requires an imatrix" in L.qs_last_error()
+    required = {"iq2_xxs", "iq2_xs", "iq2_s"}
+    assert {n for n, sp in qs.ALL_SPECS.items() if sp.needs_imatrix} == required | {"iq3_xxs"}
+    for name in required:
+        assert _call(L, int(qs.ALL_SPECS[name].ggml_type)) == -22, name
+        assert b"requires an imatrix" in L.qs_last_error(), name
+    if L.qs_device_count() == 0:        # with a device the call would launch on the dummy pointers
+        assert _call(L, int(qs.ALL_SPECS["iq3_xxs"].ggml_type)) != 0
+        assert b"requires an imatrix" not in L.qs_last_error()
 
 
 def test_cpu_quant_fn_needs_a_rocm_device(qs):

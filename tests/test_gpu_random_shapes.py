@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 TYPE_BLOCK = {"q4_0": 32, "q4_1": 32, "q5_0": 32, "q5_1": 32, "q8_0": 32, "iq4_nl": 32,
               "q2_k": 256, "q3_k": 256, "q4_k": 256, "q5_k": 256, "q6_k": 256, "iq4_xs": 256,
               "iq2_xxs": 256, "iq2_xs": 256, "iq2_s": 256, "iq3_xxs": 256, "iq3_s": 256}
-NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
+NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s"}     # IQ3_XXS runs without one (iq3_xxs.py:41-42)
 IGNORES_IMATRIX = {"q4_0", "q4_1", "q5_0", "q5_1", "q8_0"}
 SOURCES = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
 
