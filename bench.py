@@ -52,7 +52,7 @@ OUT_BYTES_PER_256 = {"q4_0": 144, "q2_k": 84, "q3_k": 110, "q4_k": 144, "q5_k": 
 TYPE_IDS = {"q4_0": 2, "q2_k": 10, "q3_k": 11, "q4_k": 12, "q5_k": 13, "q6_k": 14, "iq4_xs": 23,
             "iq2_xxs": 16, "iq2_xs": 17, "iq2_s": 22, "iq3_xxs": 18, "iq3_s": 21,
             "q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
-NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs"}
+NEEDS_IMATRIX = {"iq2_xxs", "iq2_xs", "iq2_s"}   # IQ3_XXS also runs without one (timed both ways)
 IGNORE_IMATRIX = {"q4_0", "q4_1", "q5_0", "q5_1", "q8_0"}
 B32_TYPES = IGNORE_IMATRIX          # the 32-value formats: HBM-bound, compared with a copy
 BLOCK_VALUES = {t: (32 if t in IGNORE_IMATRIX | {"iq4_nl"} else 256) for t in OUT_BYTES_PER_256}
