@@ -345,7 +345,7 @@ def cpu_baseline(oracle, host, qws, gpu_out: dict, seconds_per_type: float):
             "per_type": per_type}
 
 
-def config_c1(torch, qs, dev, steps: int) -> dict:
+def q4_0_outlier_tensor(torch, qs, dev, steps: int) -> dict:
     """Q4_0 on one 4096x4096 bf16 tensor, N(0, 0.02) with 0.1% of the values
     (16,777, chosen with seed 0) scaled x20, no imatrix; 32 distinct copies
     (1 GiB) rotate so the MALL cannot hold them."""
@@ -366,7 +366,7 @@ def config_c1(torch, qs, dev, steps: int) -> dict:
             "hbm_frac": round(alg / (per[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
-def config_c4(torch, qs, dev, steps: int) -> dict:
+def iq2_xxs_ffn_down_tensors(torch, qs, dev, steps: int) -> dict:
     """IQ2_XXS + imatrix on 36 ffn_down tensors of 2560x9728 bf16: Student-t
     (df 5) weights scaled to std 0.02, a log-normal imatrix per tensor. One
     step = the 36 tensors."""
@@ -691,14 +691,14 @@ def main() -> int:
     configs = {}
     if not args.no_configs:
         del xs_rot
-        configs["c1_q4_0_4096x4096"] = config_c1(torch, qs, dev, args.steps)
-        configs["c4_iq2_xxs_imat_36x2560x9728_student_t"] = config_c4(torch, qs, dev, args.steps)
+        configs["q4_0_4096x4096_outliers"] = q4_0_outlier_tensor(torch, qs, dev, args.steps)
+        configs["iq2_xxs_imat_36x2560x9728_student_t"] = iq2_xxs_ffn_down_tensors(torch, qs, dev, args.steps)
         torch.cuda.empty_cache()
     if "q4_0" in sel:
         per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
     for row, alg_b in [(per_type.get("q4_0 token_embd 151936x2560"),
                         algorithmic_bytes("q4_0", 151936 * 2560, 2560) - 4 * 2560),
-                       (configs.get("c1_q4_0_4096x4096"),
+                       (configs.get("q4_0_4096x4096_outliers"),
                         algorithmic_bytes("q4_0", 4096 * 4096, 4096) - 4 * 4096)]:
         if row:
             row["copy_frac"] = round(row["hbm_frac"] * HBM_PEAK_GBS / copy_peak_gbs, 4)
@@ -754,8 +754,9 @@ def main() -> int:
         head = cb["per_type"].get("q4_k+imat")
         line["identical_pct_vs_oracle"] = None if head is None else head["identical_pct"]
     if not args.no_e2e:
-        # the command line end to end on the synthetic 4B-class model (BASELINE
-        # configs 3 and the full-model IQ2_XXS run), warm and cold page cache;
+        # the command line end to end on the synthetic 4B-class model (the
+        # Q4_K_M mix with --mem 4G and the full-model IQ2_XXS run), warm and
+        # cold page cache;
         # supplementary to the headline, so a failure is reported in the line
         try:
             line["e2e"] = e2e_runs(torch, dev, ["IQ2_XXS", "Q4_K_M --mem 4G"], args.e2e_dir)

@@ -87,7 +87,7 @@ int qs_init(int device);
  *   QS_SQRT_IEEE           the correctly rounded root (torch.sqrt on a GPU
  *                          tensor, as on the reference's CUDA path; C sqrtf)
  *   QS_SQRT_TORCH_CPU_AMD  torch.sqrt on a CPU tensor on an AMD EPYC host (the
- *                          MI355X box's; MKL there: one ulp below on 7.4% and
+ *                          MI355X machine's; MKL there: one ulp below on 7.4% and
  *                          one ulp above on 9.8% of the classes of normal
  *                          inputs, the IEEE root on every subnormal input)
  * Process-wide; read by each qs_quantize() call at launch. */

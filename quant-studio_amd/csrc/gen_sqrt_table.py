@@ -19,7 +19,7 @@ oracle uses the same table, and tests/test_oracle.py re-checks it against
 torch.sqrt on random normal, subnormal and special inputs.
 
 The rounding is a property of the host's MKL, not of torch: on an AMD EPYC
-host (the MI355X box's) the same torch build returns the IEEE root on 82.9%
+host (an MI355X machine's) the same torch build returns the IEEE root on 82.9%
 of the keys, one ulp below on 7.4% and one ulp above on 9.8%, again a
 function of the key alone and the same under every ATEN_CPU_CAPABILITY. That
 host's rounding is kept as a 2-bit map per key (`--write-map`: 0 = IEEE root,

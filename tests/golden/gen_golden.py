@@ -113,14 +113,14 @@ def make_cases() -> dict[str, dict[str, np.ndarray]]:
     a[13, :] = np.where(rng.random(k) < 0.5, 0.02, -0.02)
     cases["synth"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
 
-    # C2-like: N(0, 0.02) with log-normal per-row std jitter, 0.1% outliers x20
+    # ffn-like: N(0, 0.02) with log-normal per-row std jitter, 0.1% outliers x20
     rows, k = 64, 512
     a = rng.standard_normal((rows, k)) * 0.02 * np.exp(0.3 * rng.standard_normal((rows, 1)))
     idx = rng.choice(rows * k, rows * k // 1000, replace=False)
     a.reshape(-1)[idx] *= 20.0
     cases["normal"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))
 
-    # C4-like: Student-t df=5 scaled to std 0.02
+    # heavy-tailed: Student-t df=5 scaled to std 0.02
     rows, k = 32, 512
     a = rng.standard_t(5, (rows, k)) * 0.02 / np.sqrt(5.0 / 3.0)
     cases["student"] = dict(x=bf16_round(a), imat=rng.lognormal(0.0, 1.0, k).astype(np.float32))

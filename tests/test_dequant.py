@@ -16,7 +16,7 @@ import dequant
 import oracle
 from golden_data import TYPES, as_f32, block_identical, cases
 
-# relative RMSE bound per type on the C2-like golden case (measured error x ~1.3)
+# relative RMSE bound per type on the ffn-like ("normal") golden case (measured error x ~1.3)
 REL_RMSE_MAX = {"q4_0": 0.15, "q2_k": 0.37, "q3_k": 0.21, "q4_k": 0.11, "q5_k": 0.055,
                 "q6_k": 0.03, "iq4_xs": 0.125, "iq2_xxs": 0.62, "iq2_xs": 0.52, "iq2_s": 0.46,
                 "iq3_xxs": 0.30, "iq3_s": 0.27}

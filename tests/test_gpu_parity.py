@@ -60,7 +60,7 @@ def test_golden_vectors(qs, dev, qtype):
         assert np.array_equal(got, ref), f"{qtype} {key}: differs from the oracle"
 
 
-def c2_like(rows: int, k: int, seed: int):
+def ffn_like(rows: int, k: int, seed: int):
     rng = np.random.default_rng(seed)
     a = rng.standard_normal((rows, k)) * 0.02 * np.exp(0.3 * rng.standard_normal((rows, 1)))
     return bf16_bits(a), rng.lognormal(0.0, 1.0, k).astype(np.float32)
@@ -73,7 +73,7 @@ def test_oracle_parity_random(qs, dev, qtype, imat):
     reference's Q4_0, q4_0.py:36-37), the IQ2 types refuse to run without one
     (their quantizers index qw unconditionally) and IQ3_XXS runs without one
     as quantize_iq3_xxs(x, None) does (iq3_xxs.py:41-42)."""
-    x, qw = c2_like(384, 2560, seed=sum(map(ord, qtype)) * 2 + int(imat))
+    x, qw = ffn_like(384, 2560, seed=sum(map(ord, qtype)) * 2 + int(imat))
     qw = qw if imat else None
     print(f"{qtype} imat={imat} 384x2560", flush=True)
     if qtype in NEEDS_IMATRIX and not imat:
@@ -105,7 +105,7 @@ def test_q4_k_imatrix_full_ffn_shapes(qs, dev):
     per-row log-normal std jitter, log-normal per-column imatrix."""
     for rows, k, seed in ((9728, 2560, 1), (2560, 9728, 2)):
         print(f"q4_k imat {rows}x{k}", flush=True)
-        x, qw = c2_like(rows, k, seed)
+        x, qw = ffn_like(rows, k, seed)
         got = hip_quantize(qs, "q4_k", x, qw, dev)
         ref = oracle.quantize("q4_k", x, qw, n_threads=NTHREADS)
         same = block_identical(got, ref, "q4_k")
@@ -114,7 +114,7 @@ def test_q4_k_imatrix_full_ffn_shapes(qs, dev):
 
 @pytest.mark.parametrize("qtype", ["q4_0", "q4_k", "q6_k", "q3_k", "iq2_xxs", "iq2_s", "iq3_s"])
 def test_row_chunking_invariance(qs, dev, qtype):
-    x, qw = c2_like(300, 1024, seed=9)
+    x, qw = ffn_like(300, 1024, seed=9)
     tid = TYPES[qtype][0]
     xd = to_device(x, dev)
     q = torch.from_numpy(qw).to(dev)
@@ -136,7 +136,7 @@ def test_f16_source(qs, dev, qtype):
 
 
 def test_row_stride_and_unaligned_output(qs, dev):
-    x, qw = c2_like(40, 1024, seed=12)
+    x, qw = ffn_like(40, 1024, seed=12)
     wide = torch.zeros((40, 1024 + 64), dtype=torch.bfloat16, device=dev)
     wide[:, :1024] = to_device(x, dev)
     view = wide[:, :1024]                       # row stride 1088 elements (2176 B)
@@ -156,7 +156,7 @@ def test_row_stride_and_unaligned_output(qs, dev):
 def test_empty_and_single_row(qs, dev):
     e = torch.zeros((0, 256), dtype=torch.bfloat16, device=dev)
     assert qs.quantize(12, e, None).shape == (0, 144)
-    x, qw = c2_like(1, 256, seed=3)
+    x, qw = ffn_like(1, 256, seed=3)
     got = hip_quantize(qs, "q4_k", x, qw, dev)
     assert np.array_equal(got, oracle.quantize("q4_k", x, qw))
 
@@ -213,7 +213,7 @@ def test_sqrt_rounding_modes(qs, dev, mode, qtype, imat):
     IEEE root, and torch.sqrt as an AMD EPYC host's MKL rounds it (the map the
     library embeds, decoded independently by the test)."""
     import sqrt_hosts
-    x, qw = c2_like(192, 2560, seed=77 + sum(map(ord, qtype)))
+    x, qw = ffn_like(192, 2560, seed=77 + sum(map(ord, qtype)))
     qw = qw if imat else None
     print(f"{qtype} imat={imat} sqrt={mode}", flush=True)
     if mode == "ieee":
@@ -242,7 +242,7 @@ def test_cpu_device_quant_fn(qs, dev, qtype):
     """make_kernel(cpu, qw) returns a quant_fn that takes CPU tensors and
     returns a CPU uint8 tensor with the oracle's bytes (the reference's CPU
     path, quant-studio.py:216-232), computing on the ROCm device."""
-    x, qw = c2_like(33, 512, seed=5)
+    x, qw = ffn_like(33, 512, seed=5)
     spec = qs.QUANT_TYPES[qtype]
     fn = spec.make_kernel(torch.device("cpu"), torch.from_numpy(qw))
     xt = torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16)
@@ -259,7 +259,7 @@ def test_layouts_the_c_call_refuses_are_copied(qs, dev):
     """Views the C call does not take (column offset not 16-byte aligned, row
     stride not a multiple of 16 bytes, an expanded row) are quantized from a
     contiguous copy: same bytes as the contiguous tensor."""
-    x, qw = c2_like(24, 512, seed=8)
+    x, qw = ffn_like(24, 512, seed=8)
     base = torch.zeros((24, 512 + 40), dtype=torch.bfloat16, device=dev)
     base[:, 1:513] = to_device(x, dev)
     odd = torch.zeros((24, 516), dtype=torch.bfloat16, device=dev)
@@ -283,7 +283,7 @@ def test_init_uploads_tables_up_front(qs, dev):
     behaves as before on every table it uploaded."""
     qs.init(0)
     qs.init(0)
-    x, qw = c2_like(16, 512, seed=6)
+    x, qw = ffn_like(16, 512, seed=6)
     for qtype in ("q4_k", "iq2_s", "iq3_s"):
         assert np.array_equal(hip_quantize(qs, qtype, x, qw, dev),
                               oracle.quantize(qtype, x, qw, n_threads=NTHREADS))

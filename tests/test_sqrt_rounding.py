@@ -1,7 +1,7 @@
 """The reference's square root rounds differently on different hosts (torch.sqrt
 on a CPU tensor goes through the host's MKL): the library reproduces an Intel
 host (the default, where the golden vectors were written), an AMD EPYC host
-(the MI355X box's) or the IEEE root. These CPU tests pin the embedded AMD map
+(the host of an MI355X machine) or the IEEE root. These CPU tests pin the embedded AMD map
 and prove its lookup band; test_host_sqrt_rounding checks the running host's
 torch against the tables."""
 
@@ -15,7 +15,7 @@ import pytest
 import oracle
 import sqrt_hosts
 
-# the map measured on the MI355X box's host (AMD EPYC, torch 2.10.0+rocm7.0,
+# the map measured on an MI355X machine's host (AMD EPYC, torch 2.10.0+rocm7.0,
 # oneAPI MKL 2024.2) by gen_sqrt_table.py
 AMD_MAP_SHA256 = "3e49f6e5c17392c0788450ff06ee602787215ebd84301e185ef6ff4e1bd41903"
 AMD_COUNTS = {-1: 1239767, 0: 13900284, 1: 1637165}
@@ -101,9 +101,9 @@ def test_host_sqrt_rounding():
 
 
 @pytest.mark.gpu
-def test_gpu_box_host_sqrt_rounding():
-    """The same check on the GPU box's host CPU (the host whose rounding
-    torch-cpu-amd records)."""
+def test_gpu_host_sqrt_rounding():
+    """The same check on the host CPU of the machine that holds the GPU (an
+    AMD EPYC host, whose rounding torch-cpu-amd records)."""
     torch = pytest.importorskip("torch")
     name = sqrt_hosts.host_rounding_matches(torch)
-    print(f"GPU box host torch.sqrt: {name}", flush=True)
+    print(f"GPU host torch.sqrt: {name}", flush=True)
