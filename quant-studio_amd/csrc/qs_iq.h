@@ -55,11 +55,13 @@ struct alignas(16) IqLds {
     float sc[SPW][16];
 };
 
-template <int SPW, int BYTES>
+// (a workgroup of several waves may hold waves past the last superblock:
+// they store nothing)
+template <int SPW, int BYTES, int WPG = 1>
 QS_DEV void sb_store(const IqLds<SPW, BYTES>& s, const KArgs& a) {
-    const int64_t first = (int64_t)blockIdx.x * SPW;
+    const int64_t first = grid_wave<WPG>() * SPW;
     const int64_t nvalid = min((int64_t)SPW, a.n_units - first);
-    store_staged(s.out, a.dst, first * BYTES, (int)nvalid * BYTES);
+    if (WPG == 1 || nvalid > 0) store_staged<(WPG > 1)>(s.out, a.dst, first * BYTES, (int)nvalid * BYTES);
 }
 
 template <int I, int END, typename F>
@@ -72,10 +74,10 @@ QS_DEV void static_for(F&& f) {
 
 // Grid levels staged in LDS as bytes 2l+1 (4 per word, NV/4 words per grid
 // point), so a level is one byte-to-float conversion.
-template <int BITS, int NV, int GS>
+template <int BITS, int NV, int GS, int THREADS = 64>
 QS_DEV void stage_levels(const uint16_t* grid, uint32_t* glv) {
     constexpr int W = NV / 4;
-    for (int i = threadIdx.x; i < GS * W; i += 64) {
+    for (int i = threadIdx.x; i < GS * W; i += THREADS) {
         const uint32_t code = grid[i / W];
         uint32_t word = 0;
 #pragma unroll
@@ -217,12 +219,12 @@ QS_DEV void iq_load_chunk(const IqTabDev& T, size_t chunk, uint32_t (&wd)[CH / 2
     }
 }
 
-template <int BITS, int NV, int OFF, int CH, int MAXCH, int N>
+template <int BITS, int NV, int OFF, int CH, int MAXCH, bool WL = false, int N>
 QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, unsigned long long* res,
                      const float (&xv)[N], const float (&wv)[N], float sc, uint32_t ci, bool want,
                      bool& on) {
     static_assert(CH == 4 || CH == 8, "chunks are one 8- or 16-byte load");
-    const int lane = threadIdx.x;
+    const int lane = WL ? lane_id() : (int)threadIdx.x;
     on = (ci & CI_ON_GRID) != 0;
     const int n = (on || !want) ? 0 : (int)(ci & 0xfffu);
     // IQ3: the list's first chunk is evaluated by its own lane, loaded here,
@@ -255,7 +257,7 @@ QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, uns
         }
         best_own = iq_chunk_best<BITS, NV, CH>(glds, own, 0, n, sc, xs, ws);
     }
-    wave_sync();
+    wave_sync<WL>();
     for (int base = 0; base < total; base += 64) {
         const int c = base + lane;
         const bool have = c < total;
@@ -277,7 +279,7 @@ QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, uns
             atomicMin(&res[owner], iq_chunk_best<BITS, NV, CH>(glds, wd, kc, o_n, o_sc, xs, ws));
         }
     }
-    wave_sync();
+    wave_sync<WL>();
     if (on) return (int)(ci & 0xffffu);
     const unsigned long long r0 = res[lane];
     const unsigned long long r = r0 < best_own ? r0 : best_own;
@@ -413,7 +415,7 @@ struct IqSteps {
     int n;
 };
 
-template <int SRC, int LPS, int GROUP, int SQ>
+template <int SRC, int LPS, int GROUP, int SQ, bool WL = false>
 QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K], float (*tmp)[40],
                             float sig_mult, bool use_x2, float (&x)[GROUP], float (&w)[GROUP]) {
     constexpr int SPW = 64 / LPS;
@@ -423,7 +425,7 @@ QS_DEV void iq_load_weights(const KArgs& a, const SbPos& p, float (*vlds)[QK_K],
         for (int i = 0; i < GROUP; i++) w[i] = x[i] * x[i];
         return;
     }
-    const float sum = sb_sumsq_halves<LPS, SPW, GROUP>(vlds, tmp, x, p.slot, p.g);
+    const float sum = sb_sumsq_halves<LPS, SPW, GROUP, WL>(vlds, tmp, x, p.slot, p.g);
     const float sigma2 = (sig_mult == 2.0f ? 2.0f * sum : sum) / 256.0f;
     imatrix_weights<GROUP, true, SQ>(a.qw + p.col, sigma2, x, a.sqrt, w);
 }
@@ -537,22 +539,34 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
 // IQ2_XS / IQ2_S  scale_search iq2xs_common.py:280-342; quantize_iq2_xs
 // iq2_xs.py:20-69; quantize_iq2_s iq2_s.py:21-62
 // ------------------------------------------------------------------
-template <int SRC, bool IS_S, int SQ>
-// IQ2_XS fits 4 waves per SIMD in 128 VGPRs without spills (8% faster than
-// 3); IQ2_S is held to 3 by its LDS (the 1024-entry grid) and spills at 128
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4))) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
+template <int SRC, bool IS_S, int SQ, int WPG>
+// WPG waves per workgroup share one staged grid (4 / 8 KB) and keep their own
+// search and output buffers; each wave quantizes its own superblocks and
+// syncs only with itself once the grid is staged. IQ2_S (8 KB of grid, 12.4
+// KB of LDS per one-wave workgroup, 156 VGPRs: 3 waves per SIMD) runs 4
+// waves per workgroup at 6.3 KB of LDS and 128 VGPRs per wave (4 waves per
+// SIMD, 20 spilled): 6% faster. IQ2_XS fits 4 waves per SIMD in one-wave
+// workgroups already (127 VGPRs, 10.1 KB) and stays there (1% slower with 4)
+__global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S && WPG == 1 ? 3 : 4))) void k_iq2_xs_s(KArgs a, IqTabDev T, IqSteps sweep) {
     constexpr int LPS = 16, SPW = 4, BYTES = IS_S ? 82 : 74, GS = IS_S ? 1024 : 512;
-    __shared__ IqLds<SPW, BYTES> s;
-    __shared__ __align__(16) uint32_t glds[GS * 2];
-    __shared__ int wlds[SPW][16][2];
     constexpr int MAXCH = IS_S ? IQ2_1024_MAXCH : IQ2_512_MAXCH;
-    __shared__ uint8_t cmap[64 * MAXCH];
-    __shared__ unsigned long long res[64];
-    stage_levels<2, 8, GS>(T.grid, glds);
-    const SbPos p = sb_pos<LPS, 16>(a.n_units, a.units_per_row, a.stride);
+    __shared__ IqLds<SPW, BYTES> s_w[WPG];
+    __shared__ __align__(16) uint32_t glds[GS * 2];
+    __shared__ int wlds_w[WPG][SPW][16][2];
+    __shared__ uint8_t cmap_w[WPG][64 * MAXCH];
+    __shared__ unsigned long long res_w[WPG][64];
+    const int wave = (int)(threadIdx.x >> 6);
+    IqLds<SPW, BYTES>& s = s_w[wave];
+    int (*wlds)[16][2] = wlds_w[wave];
+    uint8_t* cmap = cmap_w[wave];
+    unsigned long long* res = res_w[wave];
+    constexpr bool WL = WPG > 1;
+    stage_levels<2, 8, GS, 64 * WPG>(T.grid, glds);
+    if constexpr (WL) __syncthreads();            // the grid is every wave's
+    const SbPos p = sb_pos<LPS, 16, WPG>(a.n_units, a.units_per_row, a.stride);
     const int slot = p.slot, g = p.g;
     float x[16], w[16], waux[16], xval[16];
-    iq_load_weights<SRC, LPS, 16, SQ>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
+    iq_load_weights<SRC, LPS, 16, SQ, WL>(a, p, s.v, s.tmp, IS_S ? 2.0f : 1.0f, false, x, w);
     sqrt_ref_n<16, true, SQ>(w, a.sqrt, waux);
     int signs[2];
     if constexpr (IS_S) {
@@ -578,8 +592,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
         bool on[2];
         uint32_t ci[2];
         iq_codes<2, 8, 2>(T, xval, inv, ci);
-        gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
-        gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
+        gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
+        gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -600,9 +614,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
         bool on;
         uint32_t ci[2];
         iq_codes<2, 8, 2>(T, xval, inv, ci);
-        const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[0],
+        const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
                                                           need && !og[0], on);
-        const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[1],
+        const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
                                                           need && !og[1], on);
         if (need && !og[0]) win[0] = r0;
         if (need && !og[1]) win[1] = r1;
@@ -620,7 +634,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
     s.sc[slot][g] = active ? scale : 0.0f;
     wlds[slot][g][0] = active ? win[0] : 0;
     wlds[slot][g][1] = active ? win[1] : 0;
-    wave_sync();
+    wave_sync<WL>();
     float d;
     bool has;
     int l[16];
@@ -661,8 +675,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IS_S ? 3 : 4
             o[74 + g] = (uint8_t)(has ? (l[2 * g] | (l[2 * g + 1] << 4)) : 0);
         }
     }
-    wave_sync();
-    sb_store(s, a);
+    wave_sync<WL>();
+    sb_store<SPW, BYTES, WPG>(s, a);
 }
 
 // ------------------------------------------------------------------

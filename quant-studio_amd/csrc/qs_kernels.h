@@ -281,7 +281,7 @@ QS_DEV void sb_store(const SbLds<SPW, BYTES, VSB>& s, const KArgs& a) {
 // wave's superblocks at a time (half the LDS). Every lane takes part in both
 // rounds, the wave barriers included; lanes of the other half compute the
 // same sums from the same staged values and discard them.
-template <int LPS, int SPW, int GROUP>
+template <int LPS, int SPW, int GROUP, bool WL = false>
 QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x)[GROUP], int slot, int g) {
     static_assert(GROUP * LPS == QK_K, "the lanes of a superblock cover its values");
     constexpr int H = SPW / 2;
@@ -294,10 +294,10 @@ QS_DEV float sb_sumsq_halves(float (*v)[QK_K], float (*tmp)[40], const float (&x
 #pragma unroll
             for (int i = 0; i < GROUP; i++) v[hs][GROUP * g + i] = x[i] * x[i];
         }
-        wave_sync();
-        const float t = sb_cascade8_256<LPS>(v[hs], tmp[hs], g);
+        wave_sync<WL>();
+        const float t = sb_cascade8_256<LPS, WL>(v[hs], tmp[hs], g);
         sum = mine ? t : sum;
-        wave_sync();                          // the next round restages v and tmp
+        wave_sync<WL>();                          // the next round restages v and tmp
     }
     return sum;
 }

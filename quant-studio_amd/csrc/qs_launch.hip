@@ -136,11 +136,14 @@ hipError_t launch_type(int type, bool imat, const qs::KArgs& a, hipStream_t st,
         return launch(k_iq2_xxs<SRC, SQ>, sb8, wave, st, a, tabs[IQT_G2_256], qp4, sweep);
     }
     case QS_TYPE_IQ2_XS:      // SWEEP_CS iq2xs_common.py:21
-        return launch(k_iq2_xs_s<SRC, false, SQ>, sb4, wave, st, a, tabs[IQT_G2_512],
+        return launch(k_iq2_xs_s<SRC, false, SQ, 1>, sb4, wave, st, a, tabs[IQT_G2_512],
                       iq_steps(5.0f, 0.1f, -9, 9));
-    case QS_TYPE_IQ2_S:
-        return launch(k_iq2_xs_s<SRC, true, SQ>, sb4, wave, st, a, tabs[IQT_G2_1024],
+    case QS_TYPE_IQ2_S: {     // four waves per workgroup share the 1024-entry grid
+        constexpr int WPG = 4;
+        const dim3 g((unsigned)((a.n_units + 4 * WPG - 1) / (4 * WPG)));
+        return launch(k_iq2_xs_s<SRC, true, SQ, WPG>, g, dim3(64 * WPG), st, a, tabs[IQT_G2_1024],
                       iq_steps(5.0f, 0.1f, -9, 9));
+    }
     case QS_TYPE_IQ3_XXS: {    // _STEPS iq3_xxs.py:22
         const dim3 sb2((unsigned)((a.n_units + 1) / 2));
         return imat ? launch(k_iq3<SRC, false, true, SQ, 4>, sb2, wave, st, a, tabs[IQT_G3_256],
