@@ -58,9 +58,10 @@ def host_rows(x: torch.Tensor, rows: list[int]) -> np.ndarray:
 
 
 # one type per kernel family / launch shape: 256 blocks of 32 per 256-thread
-# workgroup (k_b32), 64 blocks per wave (IQ4_NL), 8 / 4 / 2 superblocks per wave
+# workgroup (k_b32), 64 blocks per wave (IQ4_NL), 8 / 4 / 2 superblocks per
+# one-wave workgroup, and 16 superblocks per four-wave workgroup (IQ2_S)
 CASES = [("q4_0", False), ("iq4_nl", True), ("q4_k", True), ("q6_k", True),
-         ("iq2_xs", True), ("iq3_xxs", True)]
+         ("iq2_xs", True), ("iq2_s", True), ("iq3_xxs", True)]
 
 
 @pytest.mark.parametrize("qtype,imat", CASES)
