@@ -141,7 +141,7 @@ def test_row_stride_and_unaligned_output(qs, dev):
     wide[:, :1024] = to_device(x, dev)
     view = wide[:, :1024]                       # row stride 1088 elements (2176 B)
     assert view.stride(0) == 1088
-    for qtype in ("q4_0", "q6_k", "q4_k", "iq2_xxs", "iq3_s"):
+    for qtype in ("q4_0", "q6_k", "q4_k", "iq2_xxs", "iq2_s", "iq3_s"):
         tid = TYPES[qtype][0]
         rb = TYPES[qtype][2] * (1024 // TYPES[qtype][1])
         buf = torch.zeros(40 * rb + 3, dtype=torch.uint8, device=dev)
