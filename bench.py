@@ -662,8 +662,8 @@ def main() -> int:
     for qtype in sel:
         for imat in modes_of(qtype):
             key = f"{qtype}{'+imat' if imat else ''}"
-            # 20 warm-up steps: after 5 the kernels still ran up to 5% slower
-            # than after the headline's long warm-up
+            # 20 warm-up steps; the rows still run 2-5% slower than the same
+            # kernel after the headline's 300
             st, km = time_steps(torch, shape_launches(qs, qtype, imat, xs_rot, qws, outs_for(qtype)),
                                 max(10, args.steps // 4), 20)
             a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
