@@ -33,7 +33,13 @@ enum { MUT_IEEE_RDIV = 1, MUT_SEQ_CASCADE = 2, MUT_SEQ_TREE = 3, MUT_DROP_STEP =
        MUT_ROUND_AWAY = 5, MUT_ACCEPT_GE = 6,
        /* the 32-value formats without a reference module: d = a * (1/n) instead of
         * the IEEE a / n, and x / d instead of x * (1/d) */
-       MUT_D_BY_RECIP = 7, MUT_X_DIV_D = 8 };
+       MUT_D_BY_RECIP = 7, MUT_X_DIV_D = 8,
+       /* slips that only zero imatrix weights expose (every distance or error
+        * ties at 0, a sum of squares is exactly 0): the last of equal neighbour
+        * distances kept, make_qp's candidate accept with <=, make_qx's first
+        * scale divided without its zero guard, IQ2_XXS active without
+        * scale0*3 > 0 */
+       MUT_IQ_LAST_MIN = 9, MUT_QP_ACCEPT_LE = 10, MUT_QX_NO_GUARD = 11, MUT_IQ2XXS_NO_EFF = 12 };
 
 /* torch: python_float / tensor  ->  tensor.reciprocal() * python_float */
 static inline float RDIV(float c, float t) {
@@ -381,7 +387,7 @@ static void make_qp(const float *x, const float *w, int n, int nmax, int f64_ste
             tmp[i] = w[i] * (d * d);
         }
         float mse = qso_sum_cascade8(tmp, n);
-        if (mse < best_mse) { best_mse = mse; iscale = isc; }
+        if (mse < best_mse || (g_mut == MUT_QP_ACCEPT_LE && mse == best_mse)) { best_mse = mse; iscale = isc; }
     }
     for (int i = 0; i < n; i++) L[i] = fminf(RINT(iscale * x[i]), fmax);
     float t2[32];
@@ -425,7 +431,7 @@ static void make_qx(const float *x, const float *w, int n, int nmax, float *scal
     for (int i = 0; i < n; i++) L[i] = clampf(RINT(iscale * x[i]), -fmax, fmax - 1.0f);
     for (int i = 0; i < n; i++) { tmp[i] = (w[i] * x[i]) * L[i]; t2[i] = (w[i] * L[i]) * L[i]; }
     float sumlx = sum_seq(tmp, n), suml2 = sum_seq(t2, n);
-    float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
+    float scale = (suml2 != 0 || g_mut == MUT_QX_NO_GUARD) ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
     for (int s = 0; s < 18; s++) {
         float isc = RDIV(-steps[s], mxs);

@@ -113,7 +113,7 @@ static int nearest(const IqTab *T, int code, const float *xv, const float *wv, f
             float t = (wv[j] * diff) * diff;
             d2 = (n == 4 && j == 0) ? t : d2 + t;
         }
-        if (d2 < best) { best = d2; besti = gi; }
+        if (d2 < best || (g_mut == MUT_IQ_LAST_MIN && d2 == best)) { best = d2; besti = gi; }
     }
     return besti;
 }
@@ -209,7 +209,7 @@ static void iq2_xxs_block(const float *x, const float *qw, uint8_t *out) {
         float scale0;
         make_qp(xval, wg, 32, 4, 1, &scale0, NULL);
         float eff = scale0 * 3.0f;
-        active = active && eff > 0;
+        active = active && (eff > 0 || g_mut == MUT_IQ2XXS_NO_EFF);
         float eff_safe = active ? eff : 1.0f;
         float scale = scale0, best = 0.0f;
         int L[4] = {-1, -1, -1, -1};                 /* grid index per subgroup; -1 = zero levels */

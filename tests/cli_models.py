@@ -66,18 +66,28 @@ def small_model(path: Path, seed: int = 42, odd: bool = True) -> dict[str, np.nd
     return expect
 
 
-def imatrix_for(path: Path, names_k: dict[str, int], seed: int = 7, n_mat: dict | None = None) -> dict:
-    """imatrix GGUF: <name>.in_sum2 = v * count per column, <name>.counts = [count]."""
+def imatrix_for(path: Path, names_k: dict[str, int], seed: int = 7, n_mat: dict | None = None,
+                zero_frac: float = 0.0, dead_counts: dict | None = None) -> dict:
+    """imatrix GGUF: <name>.in_sum2 = v * count per column, <name>.counts = [count].
+    zero_frac: that fraction of the columns, and every other 16-column group,
+    never fired (in_sum2 = 0); dead_counts: {name: [matrix indices]} whose count
+    is 0 (an expert that was never routed: its weights load as 0,
+    quant-studio.py:80-85)."""
     rng = np.random.default_rng(seed)
     tensors, values = [], {}
     for name, k in names_k.items():
         m = (n_mat or {}).get(name, 1)
         v = (rng.random(k * m).astype(np.float32) * 4.0 + 0.05)
+        if zero_frac:
+            v[rng.random(k * m) < zero_frac] = 0.0
+            v.reshape(-1, 16)[::2] = 0.0
         cnt = np.full(m, 100.0, np.float32)
+        cnt[list((dead_counts or {}).get(name, []))] = 0.0
         s = (v.reshape(m, k) * cnt[:, None]).astype(np.float32).reshape(-1)
         tensors.append((name + ".in_sum2", (k * m,), GT.F32, s))
         tensors.append((name + ".counts", (m,), GT.F32, cnt))
-        values[name] = (s.reshape(m, k) / cnt[:, None]).reshape(-1)
+        live = cnt[:, None] > 0
+        values[name] = np.where(live, s.reshape(m, k) / np.where(live, cnt[:, None], 1), 0).reshape(-1)
     io.write_gguf(path, "imatrix", [KV("general.type", VT.STRING, "imatrix")], tensors)
     return values
 

@@ -14,6 +14,7 @@ provides a minimal stand-in module exposing those names with the public GGUF
 enum values; no arithmetic depends on it.
 
 Usage: python tests/golden/gen_golden.py [--ref /root/reference] [--only TYPE ...]
+       python tests/golden/gen_golden.py --zero-imatrix   (writes zero_imat.npz only)
 """
 
 from __future__ import annotations
@@ -139,6 +140,82 @@ def make_cases() -> dict[str, dict[str, np.ndarray]]:
     return cases
 
 
+def make_zero_cases() -> dict[str, dict[str, np.ndarray]]:
+    """Imatrix vectors with zero entries, as real imatrix files give them: the
+    reference's loader writes 0 wherever a column's count is not positive
+    (quant-studio.py:80-85), and a 3-D expert tensor gets expert 0's first k
+    values (quant-studio.py:455), all zero when that expert was never routed.
+    The zeros then reach every weight formula (qw*sqrt(sigma2+x^2),
+    q4_k.py:49-51; sqrt(w) in the IQ searches, iq2.py:429-436)."""
+    cases = {}
+    rng = np.random.default_rng(20261202)
+
+    def rows_with_adversarial(rows, k, std):
+        a = rng.standard_normal((rows, k)) * std * np.exp(0.3 * rng.standard_normal((rows, 1)))
+        a[0, :] = 0.0
+        a[1, :] = 0.5
+        a[2, :] = rng.standard_normal(k) * 1e-17
+        a[3, :] = np.abs(a[3, :])
+        a[4, :] = np.round(rng.standard_normal(k) * 4) / 64.0
+        return a
+
+    # scattered zeros: about a quarter of the columns never fired
+    k = 1024
+    a = rows_with_adversarial(24, k, 0.02)
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    qw[rng.random(k) < 0.25] = 0.0
+    cases["zscatter"] = dict(x=bf16_round(a), imat=qw)
+
+    # whole zero groups: 16- and 32-value groups, a 256-value superblock, half a
+    # superblock, every other 16-group of one superblock, and 8-value subgroups
+    k = 1024
+    a = rows_with_adversarial(16, k, 0.02)
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    qw[0:16] = 0.0
+    qw[48:64] = 0.0
+    qw[64:96] = 0.0
+    qw[136:144] = 0.0
+    qw[200:204] = 0.0
+    qw[256:512] = 0.0
+    qw[512:640] = 0.0
+    for g in range(8):
+        qw[768 + 32 * g: 768 + 32 * g + 16] = 0.0
+    cases["zgroups"] = dict(x=bf16_round(a), imat=qw)
+
+    # heavy-tailed rows, half of the 8-value subgroups' columns zero
+    k = 512
+    a = rng.standard_t(5, (16, k)) * 0.02 / np.sqrt(5.0 / 3.0)
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    qw[np.repeat(rng.random(k // 8) < 0.5, 8)] = 0.0
+    cases["zsub8"] = dict(x=bf16_round(a), imat=qw)
+
+    # an all-zero vector: an expert that was never routed
+    k = 512
+    a = rows_with_adversarial(8, k, 0.02)
+    cases["zall"] = dict(x=bf16_round(a), imat=np.zeros(k, np.float32))
+    return cases
+
+
+def write_zero_imatrix(out: Path, only) -> None:
+    """zero_imat.npz: the cases of make_zero_cases and the reference's bytes for
+    every type that uses an imatrix (keys <case>.x, <case>.imat, <type>.<case>)."""
+    import importlib
+    cases = make_zero_cases()
+    rec = {}
+    for cname, c in cases.items():
+        rec[f"{cname}.x"] = c["x"]
+        rec[f"{cname}.imat"] = c["imat"]
+    for tname, mod, fn, modes in TYPES:
+        if "imat" not in modes or (only and tname not in only):
+            continue
+        f = getattr(importlib.import_module(f"kernels.{mod}"), fn)
+        for cname, c in cases.items():
+            y = f(torch.from_numpy(case_f32(c).copy()), torch.from_numpy(c["imat"].copy()))
+            rec[f"{tname}.{cname}"] = y.numpy().astype(np.uint8)
+        print(f"{tname}: zero-imatrix cases {', '.join(cases)}", flush=True)
+    np.savez_compressed(out / "zero_imat.npz", **rec)
+
+
 def case_f32(case: dict[str, np.ndarray]) -> np.ndarray:
     x = case["x"]
     return bf16_to_f32(x) if x.dtype == np.uint16 else x
@@ -149,6 +226,8 @@ def main() -> None:
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--out", default=str(HERE))
     ap.add_argument("--only", nargs="*", help="write only these types' files (inputs.npz is left as is)")
+    ap.add_argument("--zero-imatrix", action="store_true",
+                    help="write only zero_imat.npz (imatrix vectors with zero entries)")
     args = ap.parse_args()
 
     install_enum_module()
@@ -156,6 +235,9 @@ def main() -> None:
     import importlib
 
     torch.set_num_threads(1)
+    if args.zero_imatrix:
+        write_zero_imatrix(Path(args.out), args.only)
+        return
     cases = make_cases()
     inputs = {}
     for cname, c in cases.items():

@@ -50,3 +50,21 @@ def as_f32(x: np.ndarray) -> np.ndarray:
 def block_identical(a: np.ndarray, b: np.ndarray, qtype: str) -> np.ndarray:
     bb = TYPES[qtype][2]
     return (a.reshape(-1, bb) == b.reshape(-1, bb)).all(1)
+
+
+_zero = None
+
+
+def zero_imatrix_cases(qtype: str):
+    """[(case, x bf16 bits, imatrix with zero entries, expected uint8)] from
+    zero_imat.npz, written by the reference's eager quantizers
+    (gen_golden.py --zero-imatrix); empty for a type without an imatrix mode."""
+    global _zero
+    if _zero is None:
+        _zero = dict(np.load(GOLDEN / "zero_imat.npz"))
+    out = []
+    for key in sorted(_zero):
+        t, _, case = key.partition(".")
+        if t == qtype:
+            out.append((case, _zero[f"{case}.x"], _zero[f"{case}.imat"], _zero[key]))
+    return out

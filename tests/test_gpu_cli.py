@@ -87,6 +87,28 @@ def test_schemes_with_imatrix(tmp_path, scheme, ftype, extra):
     check_output(src, out, expect, ftype=ftype, imatrix=imat)
 
 
+@pytest.mark.parametrize("scheme,ftype", [("IQ2_XXS", 19), ("Q4_K_M", 15), ("IQ3_S", 26), ("Q2_K", 10)])
+def test_imatrix_with_zero_columns_and_an_unrouted_expert(tmp_path, scheme, ftype):
+    """An imatrix whose columns partly never fired (in_sum2 = 0; every other
+    16-column group and ~30% more) and whose 3-D expert tensor has a zero
+    count for expert 0, the only expert the reference reads (quant-studio.py:
+    80-85, :455): that tensor's weights are all zero. Every quantized tensor
+    equals the oracle fed the same loaded weights."""
+    src = tmp_path / "in.gguf"
+    expect = small_model(src, odd=False)
+    im = tmp_path / "im.gguf"
+    imatrix_for(im, {n: v.shape[-1] for n, v in expect.items()},
+                n_mat={"blk.0.ffn_gate_exps.weight": 4}, zero_frac=0.3,
+                dead_counts={"blk.0.ffn_gate_exps.weight": [0]})
+    imat = io.load_imatrix(im)
+    assert not imat["blk.0.ffn_gate_exps.weight"][:256].any()
+    assert (imat["blk.0.ffn_gate_exps.weight"][256:] > 0).any()
+    assert (imat["blk.0.attn_k.weight"] == 0).mean() > 0.5
+    out = tmp_path / "o.gguf"
+    run_cli(src, out, scheme, "--imatrix", im, "--mem", "128K")
+    check_output(src, out, expect, ftype=ftype, imatrix=imat)
+
+
 def test_device_cpu_writes_the_same_file(tmp_path):
     """--device cpu (the reference's CPU path) and the default device give the
     same file, byte for byte."""

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from golden_data import TYPES, block_identical, cases
+from golden_data import TYPES, block_identical, cases, zero_imatrix_cases
 
 pytestmark = pytest.mark.gpu
 
@@ -58,6 +58,44 @@ def test_golden_vectors(qs, dev, qtype):
         assert same.all(), f"{qtype} {key}: {int((~same).sum())}/{same.size} blocks differ from the reference"
         ref = oracle.quantize(qtype, x, qw, n_threads=NTHREADS)
         assert np.array_equal(got, ref), f"{qtype} {key}: differs from the oracle"
+
+
+ZERO_IMATRIX_TYPES = [t for t in HIP_TYPES if t != "q4_0"]
+
+
+@pytest.mark.parametrize("qtype", ZERO_IMATRIX_TYPES)
+def test_zero_imatrix_golden_vectors(qs, dev, qtype):
+    """Imatrix vectors with zero entries (never-fired columns, zero 8/16/32/256
+    -value groups, an all-zero vector; quant-studio.py:80-85 writes such zeros):
+    identical to the reference's own bytes and to the oracle on every block."""
+    for case, x, qw, expect in zero_imatrix_cases(qtype):
+        print(f"{qtype} zero-imatrix {case} shape={x.shape}", flush=True)
+        got = hip_quantize(qs, qtype, x, qw, dev)
+        same = block_identical(got, expect, qtype)
+        assert same.all(), f"{qtype} {case}: {int((~same).sum())}/{same.size} blocks differ from the reference"
+        assert np.array_equal(got, oracle.quantize(qtype, x, qw, n_threads=NTHREADS)), case
+
+
+@pytest.mark.parametrize("mode", ["ieee", "torch-cpu-amd"])
+@pytest.mark.parametrize("qtype", ZERO_IMATRIX_TYPES)
+def test_zero_imatrix_sqrt_modes(qs, dev, mode, qtype):
+    """The same zero-imatrix inputs in the other square-root modes, against the
+    oracle in that mode (sqrt(0) = +0 in every mode)."""
+    import sqrt_hosts
+    if mode == "ieee":
+        oracle.use_ieee_sqrt(True)
+    else:
+        oracle.use_amd_host_sqrt(sqrt_hosts.amd_ulps())
+    try:
+        qs.set_sqrt_rounding(mode)
+        for case, x, qw, _ in zero_imatrix_cases(qtype):
+            print(f"{qtype} zero-imatrix {case} sqrt={mode}", flush=True)
+            got = hip_quantize(qs, qtype, x, qw, dev)
+            assert np.array_equal(got, oracle.quantize(qtype, x, qw, n_threads=NTHREADS)), case
+    finally:
+        qs.set_sqrt_rounding("torch-cpu")
+        oracle.use_ieee_sqrt(False)
+        oracle.use_sqrt_table(None)
 
 
 def ffn_like(rows: int, k: int, seed: int):
@@ -201,9 +239,12 @@ def test_python_mirror_splits_calls_over_the_value_limit(dev, monkeypatch):
         assert np.array_equal(whole, oracle.quantize(qtype, x, qw, n_threads=NTHREADS)), qtype
 
 
-# every type whose weights take a square root: the imatrix variants, plus
-# Q4_K / Q5_K without one (av_x = sqrt(sum x^2 / 32), q4_k.py:34)
-SQRT_CASES = [(t, True) for t in HIP_TYPES + ["iq4_nl"] if t != "q4_0"] + [("q4_k", False), ("q5_k", False)]
+# every type whose weights take a square root: the imatrix variants, Q4_K /
+# Q5_K without one (av_x = sqrt(sum x^2 / 32), q4_k.py:34), and the IQ3 types
+# without one, whose searches weigh by sqrt(w) with w = x*x (iq3_xxs.py:41-47,
+# iq3_s.py:41-47)
+SQRT_CASES = [(t, True) for t in HIP_TYPES + ["iq4_nl"] if t != "q4_0"] + \
+    [("q4_k", False), ("q5_k", False), ("iq3_xxs", False), ("iq3_s", False)]
 
 
 @pytest.mark.parametrize("mode", ["ieee", "torch-cpu-amd"])

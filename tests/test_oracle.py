@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import oracle
-from golden_data import ORACLE_TYPES, block_identical, cases
+from golden_data import ORACLE_TYPES, block_identical, cases, zero_imatrix_cases
 
 
 @pytest.mark.parametrize("qtype", ORACLE_TYPES)
@@ -28,6 +28,55 @@ def test_oracle_matches_reference_golden(qtype):
         got = oracle.quantize(qtype, x, qw, n_threads=4)
         same = block_identical(got, expect, qtype)
         assert same.all(), f"{qtype} {key}: {int((~same).sum())} of {same.size} blocks differ"
+
+
+ZERO_IMATRIX_TYPES = [t for t in ORACLE_TYPES if t != "q4_0"]
+
+
+@pytest.mark.parametrize("qtype", ZERO_IMATRIX_TYPES)
+def test_oracle_matches_reference_zero_imatrix(qtype):
+    """Imatrix vectors with zero entries (columns that never fired, whole 8-,
+    16-, 32- and 256-value groups, an all-zero vector): the oracle reproduces
+    every block the reference's eager quantizers wrote for them."""
+    got_any = False
+    for case, x, qw, expect in zero_imatrix_cases(qtype):
+        assert (qw == 0).any() and (qw >= 0).all()
+        got = oracle.quantize(qtype, x, qw, n_threads=4)
+        same = block_identical(got, expect, qtype)
+        assert same.all(), f"{qtype} {case}: {int((~same).sum())} of {same.size} blocks differ"
+        got_any = True
+    assert got_any
+
+
+# planted mistakes that only zero weights expose, and the (type, case) pairs
+# of the zero-imatrix vectors that must each expose them; the first set of
+# golden vectors (strictly positive imatrix) misses 10-12 entirely and
+# catches 9 only for the IQ3 types
+ZERO_MUTANTS = {
+    9: ("neighbour search keeps the last of equal distances",
+        [("iq2_xxs", "zsub8"), ("iq2_xs", "zsub8"), ("iq2_s", "zsub8"), ("iq3_xxs", "zsub8"),
+         ("iq3_s", "zall")]),
+    10: ("make_qp accepts an equal error", [("q2_k", "zall"), ("q4_k", "zgroups"), ("q5_k", "zgroups")]),
+    11: ("make_qx's first scale without its zero guard", [("q3_k", "zgroups"), ("q6_k", "zsub8")]),
+    12: ("IQ2_XXS active without scale0*3 > 0", [("iq2_xxs", "zgroups"), ("iq2_xxs", "zsub8")]),
+}
+
+
+@pytest.mark.parametrize("mut", sorted(ZERO_MUTANTS))
+def test_zero_imatrix_vectors_catch_planted_mistake(mut):
+    what, pairs = ZERO_MUTANTS[mut]
+    L = oracle.lib()
+    L.qso_set_mutation(mut)
+    try:
+        for qtype, want in pairs:
+            hit = [c for c in zero_imatrix_cases(qtype) if c[0] == want]
+            assert hit, (qtype, want)
+            case, x, qw, expect = hit[0]
+            got = oracle.quantize(qtype, x, qw, n_threads=4)
+            assert not block_identical(got, expect, qtype).all(), \
+                f"planted mistake '{what}' not detected by {qtype} {case}"
+    finally:
+        L.qso_set_mutation(0)
 
 
 @pytest.mark.parametrize("qtype", ["q4_k", "iq2_s", "iq3_xxs"])
