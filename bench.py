@@ -6,10 +6,12 @@ Headline workload: Q4_K with an imatrix on the two ffn-shaped bf16 tensors
 jitter, sigma 0.3; per-column log-normal imatrix). One step = one quantization
 pass over both tensors (two launches), inputs already resident in HBM; the
 buffers rotate over >= 1 GiB of distinct copies so the 256 MB MALL cannot
-serve them. The GPU's clocks ramp up over the first ~100 launches, so the
-default warm-up is long enough to reach them; every launch of the timed steps
-is bracketed by HIP events on its stream, so the per-launch kernel time and
-the step time come from the same launches.
+serve them. The core clock follows VALU load, so the VALU-calibration kernel
+(~0.2 s of full-chip VALU work, measured for the line anyway) runs right
+before the headline's own warm-up and the timed launches queue behind VALU
+work. The timed steps run back to back between two HIP events on the launch
+stream; both launches of a step run the same kernel, so its average launch is
+the step time over two.
 
 The JSON line also carries:
   - per_type: every HIP type with and without imatrix on the same shapes:
@@ -129,7 +131,9 @@ def valu_peak(torch, dev, launches: int = 5) -> float:
     b.record(stream)
     torch.cuda.synchronize()
     sec = a.elapsed_time(b) * 1e-3 / launches
-    return lib.qs_calib_valu_insts(grid, iters) / sec
+    global VALU_RATE
+    VALU_RATE = lib.qs_calib_valu_insts(grid, iters) / sec
+    return VALU_RATE
 
 
 def _calib_lib():
@@ -182,10 +186,10 @@ def copy_kernel_rate(torch, dev, traffic: int, steps: int = 24) -> float:
                                ctypes.c_void_p(stream.cuda_stream))
         if rc:
             raise RuntimeError(f"qs_calib_copy failed ({rc})")
-    _, per = time_steps(torch, [launch], steps, 5)
+    _, ms = time_steps(torch, [launch], steps, 5)
     del bufs
     torch.cuda.empty_cache()
-    return 2 * n / (per[0] * 1e-3)
+    return 2 * n / (ms * 1e-3)
 
 
 def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
@@ -193,30 +197,40 @@ def algorithmic_bytes(qtype: str, n_elems: int, k: int) -> int:
     return 2 * n_elems + n_elems * OUT_BYTES_PER_256[qtype] // 256 + 4 * k
 
 
-SPIN_CYCLES_PER_S = 2.0e9      # torch.cuda._sleep's clock; measured by spin_rate() at start
+# VALU wave instructions per second of k_valu_issue on this device (set by
+# valu_peak(); before that a typical MI355X figure sizes the stream hold)
+VALU_RATE = 1.1e12
 
 
-def spin_rate(torch) -> float:
-    """Clock rate of torch.cuda._sleep's spin kernel on this device (cycles/s)."""
-    stream = torch.cuda.current_stream()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda._sleep(1000)
-    a.record(stream)
-    torch.cuda._sleep(2_000_000)
-    b.record(stream)
-    torch.cuda.synchronize()
-    return 2_000_000 / max(1e-6, a.elapsed_time(b) * 1e-3)
+def busy_hold(torch, seconds: float) -> None:
+    """Hold the current stream for about `seconds` with the VALU issue kernel
+    on every CU (libqs_calib.so). The core clock follows VALU load: after an
+    idle stretch, a one-wave spin or a memory-bound kernel, the first ~60
+    headline launches (~25 ms) ran up to 14% slower, while straight after VALU
+    work they ran at their steady rate from the first launch. So the timed
+    launches queue behind VALU work, not behind an idle spin."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "quant-studio_amd" / "_build" / "libqs_calib.so"))
+    lib.qs_calib_valu.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    grid = 8192
+    iters = max(1, int(seconds * VALU_RATE / (grid * 4 * 2 * 16)))
+    out = torch.empty(1, dtype=torch.float32, device=torch.device("cuda", torch.cuda.current_device()))
+    if lib.qs_calib_valu(grid, iters, ctypes.c_void_p(out.data_ptr()),
+                         ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) != 0:
+        raise RuntimeError("qs_calib_valu failed")
 
 
 def time_steps(torch, launches, steps: int, warmup: int):
     """Run `warmup` untimed steps, then time exactly `steps` steps, a step being
     the callables in `launches` (each queues one kernel; called with the step
-    index). Returns (ms per step, mean kernel ms per launch slot), both from
-    events on the launch stream: one before the first launch and one after
-    every launch, so consecutive events bracket one kernel each. The stream is
-    held by a short spin kernel (torch.cuda._sleep) while the timed launches
-    are queued, so kernels shorter than the host's launch cost still run back
-    to back and the brackets hold no host gaps. The hold is not timed."""
+    index). Returns (ms per step, mean ms per launch) from two events on the
+    launch stream, one before the first timed launch and one after the last;
+    the launches run back to back between them. No event sits between launches:
+    each event marker costs the command processor 2-5 us, a third of a
+    12-us kernel. The stream is held by VALU work (busy_hold) while the timed
+    launches are queued, so kernels shorter than the host's launch cost still
+    run back to back and the clock does not drop before them. The hold is not
+    timed."""
     stream = torch.cuda.current_stream()
     t0 = time.perf_counter()
     for i in range(warmup):
@@ -225,20 +239,17 @@ def time_steps(torch, launches, steps: int, warmup: int):
     # host time to queue one launch, from the warm-up (at least 50 us assumed)
     per_launch_s = max(50e-6, (time.perf_counter() - t0) / max(1, warmup * len(launches)))
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(launches) + 1)]
-          for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     hold_s = min(2.0, 2.0 * per_launch_s * steps * len(launches) + 2e-3)
-    torch.cuda._sleep(int(hold_s * SPIN_CYCLES_PER_S))
+    busy_hold(torch, hold_s)
+    e0.record(stream)
     for i in range(steps):
-        ev[i][0].record(stream)
-        for j, f in enumerate(launches):
+        for f in launches:
             f(i)
-            ev[i][j + 1].record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
-    step_ms = ev[0][0].elapsed_time(ev[-1][-1]) / steps
-    per = [sum(ev[i][j].elapsed_time(ev[i][j + 1]) for i in range(steps)) / steps
-           for j in range(len(launches))]
-    return step_ms, per
+    step_ms = e0.elapsed_time(e1) / steps
+    return step_ms, step_ms / len(launches)
 
 
 def shape_launches(qs, qtype, imat, xs_rot, qws, outs):
@@ -357,13 +368,13 @@ def q4_0_outlier_tensor(torch, qs, dev, steps: int) -> dict:
     x0 = bf16_from(torch, a).to(dev)
     xs = [x0] + [x0.clone() for _ in range(31)]
     out = torch.empty((4096, 4096 // 32 * 18), dtype=torch.uint8, device=dev)
-    wall, per = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 32], None, out=out)],
-                           max(steps, 64), 64)
+    wall, ms = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 32], None, out=out)],
+                          max(steps, 64), 64)
     alg = algorithmic_bytes("q4_0", 4096 * 4096, 4096) - 4 * 4096
     return {"workload": "Q4_0 on bf16 4096x4096, N(0,0.02) + 0.1% outliers x20, seed 0",
-            "input_GBps": round(2 * 4096 * 4096 / (per[0] * 1e-3) / 1e9, 1),
-            "kernel_ms": round(per[0], 5), "ms_per_step": round(wall, 5),
-            "hbm_frac": round(alg / (per[0] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            "input_GBps": round(2 * 4096 * 4096 / (ms * 1e-3) / 1e9, 1),
+            "kernel_ms": round(ms, 5), "ms_per_step": round(wall, 5),
+            "hbm_frac": round(alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def iq2_xxs_ffn_down_tensors(torch, qs, dev, steps: int) -> dict:
@@ -383,8 +394,7 @@ def iq2_xxs_ffn_down_tensors(torch, qs, dev, steps: int) -> dict:
         del z, c
     out = torch.empty((rows, k // 256 * 66), dtype=torch.uint8, device=dev)
     launches = [(lambda i, j=j: qs.quantize(16, xs[j], qws[j], out=out)) for j in range(n)]
-    wall, per = time_steps(torch, launches, max(1, steps // 50), 1)
-    kms = sum(per) / n
+    wall, kms = time_steps(torch, launches, max(1, steps // 50), 1)
     return {"workload": "IQ2_XXS + imatrix on 36 ffn_down tensors 2560x9728 bf16, Student-t df 5 "
                         "scaled to std 0.02, log-normal imatrix",
             "input_GBps": round(2 * rows * k * n / (wall * 1e-3) / 1e9, 2),
@@ -401,8 +411,7 @@ def q4_0_large(torch, qs, dev, steps: int) -> dict:
     g = torch.Generator(device=dev).manual_seed(1)
     xs = [(torch.randn(rows, k, device=dev, generator=g) * 0.01).to(torch.bfloat16) for _ in range(2)]
     out = torch.empty((rows, k // 32 * 18), dtype=torch.uint8, device=dev)
-    wall, per = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 2], None, out=out)], steps, 30)
-    ms = per[0]
+    wall, ms = time_steps(torch, [lambda i: qs.quantize(2, xs[i % 2], None, out=out)], steps, 30)
     alg = algorithmic_bytes("q4_0", rows * k, k) - 4 * k
     return {"input_GBps": round(2 * rows * k / (ms * 1e-3) / 1e9, 1), "kernel_ms": round(ms, 4),
             "hbm_GBps": round(alg / (ms * 1e-3) / 1e9, 1),
@@ -417,10 +426,10 @@ def copy_peak(torch, dev, steps: int, warmup: int) -> int:
     nbytes = 1 << 30
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a)
-    wall, per = time_steps(torch, [lambda i: b.copy_(a)], steps, warmup)
+    wall, ms = time_steps(torch, [lambda i: b.copy_(a)], steps, warmup)
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes,
-                      "ms_per_copy": round(per[0], 4),
-                      "copy_GBps_read_plus_write": round(2 * nbytes / (per[0] * 1e-3) / 1e9, 1)}),
+                      "ms_per_copy": round(ms, 4),
+                      "copy_GBps_read_plus_write": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}),
           flush=True)
     del a, b
     torch.cuda.empty_cache()
@@ -584,6 +593,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true", help="skip the Q4_0 4096x4096 and "
                     "IQ2_XXS Student-t workloads")
+    ap.add_argument("--configs", default="q4_0,iq2_xxs",
+                    help="which of those workloads to run: a comma list of q4_0 (4096x4096 with "
+                         "outliers) and iq2_xxs (36 Student-t ffn_down tensors)")
     ap.add_argument("--cpu-seconds", type=float, default=45.0,
                     help="CPU time per type for the identical-block check (full tensors when "
                          "the oracle fits in it)")
@@ -613,8 +625,6 @@ def main() -> int:
     qs = importlib.import_module("quant-studio_amd")
 
     dev = torch.device("cuda:0")
-    global SPIN_CYCLES_PER_S
-    SPIN_CYCLES_PER_S = spin_rate(torch)
     if args.copy_only:
         return copy_peak(torch, dev, args.steps, args.warmup)
     if args.valu_peak:
@@ -634,19 +644,29 @@ def main() -> int:
         return [torch.empty((r, k // 256 * OUT_BYTES_PER_256[qtype]), dtype=torch.uint8, device=dev)
                 for r, k in SHAPES]
 
-    # headline: Q4_K + imatrix; the dominant kernel is the 9728x2560 launch
+    # The calibration kernels run first, the VALU one last: their measurements
+    # belong to the line anyway, and the core clock follows VALU load (after
+    # idle time or memory-bound kernels the first ~60 headline launches ran up
+    # to 14% slower; straight after VALU work, at their steady rate), so ~0.2 s
+    # of VALU work right before the headline's own warm-up settles the clock
+    # whatever --warmup is.
+    copy_peak_gbs = copy_kernel_peak(torch, dev) / 1e9
+    peak_valu = valu_peak(torch, dev, launches=30)
+
+    # headline: Q4_K + imatrix; both launches of a step run the same kernel
+    # (k_q45_k, 97,280 superblocks each), so the kernel's average launch is
+    # the step time over the two launches
     ms_step, kms = time_steps(torch, shape_launches(qs, "q4_k", True, xs_rot, qws, outs_for("q4_k")),
                               args.steps, args.warmup)
     value = 2 * n_elems / (ms_step * 1e-3) / 1e9
-    print(f"bench: headline {ms_step:.4f} ms per step, {kms[0]:.4f} / {kms[1]:.4f} ms per launch",
+    print(f"bench: headline {ms_step:.4f} ms per step, {kms:.4f} ms per launch",
           file=sys.stderr, flush=True)
-    r0, k0 = SHAPES[0]
-    alg = algorithmic_bytes("q4_k", r0 * k0, k0)
-    achieved = alg / (kms[0] * 1e-3) / 1e9
+    # algorithmic bytes of the average launch (the two shapes differ only in
+    # the imatrix's 4k bytes)
+    alg = sum(algorithmic_bytes("q4_k", r * k, k) for r, k in SHAPES) // len(SHAPES)
+    achieved = alg / (kms * 1e-3) / 1e9
     insts = profile_figure("counters_q4_k_imat_9728x2560.md", "valu_insts_per_launch")
     traffic = profile_figure("counters_q4_k_imat_9728x2560.md", "traffic_bytes_per_launch")
-    peak_valu = valu_peak(torch, dev)
-    copy_peak_gbs = copy_kernel_peak(torch, dev) / 1e9
 
     per_type, gpu_out = {}, {}
     valu_counts = profiled_valu_per_type()
@@ -662,17 +682,15 @@ def main() -> int:
     for qtype in sel:
         for imat in modes_of(qtype):
             key = f"{qtype}{'+imat' if imat else ''}"
-            # 20 warm-up steps; the rows still run 2-5% slower than the same
-            # kernel after the headline's 300
             st, km = time_steps(torch, shape_launches(qs, qtype, imat, xs_rot, qws, outs_for(qtype)),
                                 max(10, args.steps // 4), 20)
-            a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (sum(km) * 1e-3) / 1e9
+            a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (st * 1e-3) / 1e9
             n_insts = valu_counts.get(key)
-            print(f"bench: {key}: {km[0]:.4f} / {km[1]:.4f} ms per launch", file=sys.stderr, flush=True)
+            print(f"bench: {key}: {km:.4f} ms per launch", file=sys.stderr, flush=True)
             per_type[key] = {
                 "input_GBps": round(2 * n_elems / (st * 1e-3) / 1e9, 2),
                 "ms_per_step": round(st, 4),
-                "kernel_ms": [round(v, 4) for v in km],
+                "kernel_ms": round(km, 4),
                 "hbm_frac": round(a / HBM_PEAK_GBS, 4),
                 "copy_frac": round(a / copy_peak_gbs, 4),
                 # against the copy kernel moving this launch's bytes (the
@@ -683,7 +701,7 @@ def main() -> int:
                 # VALU issue rate (SQ_INSTS_VALU per launch over the live launch
                 # time) against the calibration kernel's rate
                 "valu_frac": None if n_insts is None else
-                round(n_insts / (sum(km) / len(km) * 1e-3) / peak_valu, 3),
+                round(n_insts / (km * 1e-3) / peak_valu, 3),
             }
             if not args.no_cpu:
                 gpu_out[key] = gpu_bytes(torch, qs, qtype, imat, xs, qws)
@@ -691,10 +709,16 @@ def main() -> int:
         gpu_out["q4_k+imat"] = gpu_bytes(torch, qs, "q4_k", True, xs, qws)
 
     configs = {}
-    if not args.no_configs:
+    which = set() if args.no_configs else {c.strip() for c in args.configs.split(",") if c.strip()}
+    if which - {"q4_0", "iq2_xxs"}:
+        raise SystemExit(f"bench.py: unknown --configs {sorted(which - {'q4_0', 'iq2_xxs'})}")
+    if which:
         del xs_rot
-        configs["q4_0_4096x4096_outliers"] = q4_0_outlier_tensor(torch, qs, dev, args.steps)
-        configs["iq2_xxs_imat_36x2560x9728_student_t"] = iq2_xxs_ffn_down_tensors(torch, qs, dev, args.steps)
+        if "q4_0" in which:
+            configs["q4_0_4096x4096_outliers"] = q4_0_outlier_tensor(torch, qs, dev, args.steps)
+        if "iq2_xxs" in which:
+            configs["iq2_xxs_imat_36x2560x9728_student_t"] = iq2_xxs_ffn_down_tensors(torch, qs, dev,
+                                                                                       args.steps)
         torch.cuda.empty_cache()
     if "q4_0" in sel:
         per_type["q4_0 token_embd 151936x2560"] = q4_0_large(torch, qs, dev, 20)
@@ -725,8 +749,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5),
                      "traffic": None if traffic is None else int(traffic),
-                     "kernel": "k_q45_k<bf16, imatrix, 15>", "kernel_ms": round(kms[0], 4),
-                     "kernel_ms_per_shape": [round(v, 4) for v in kms],
+                     "kernel": "k_q45_k<bf16, imatrix, 15>", "kernel_ms": round(kms, 4),
                      "algorithmic_bytes": alg,
                      # the binding roof: this kernel is VALU-bound, so its
                      # SQ_INSTS_VALU per launch over the same live duration is
@@ -734,12 +757,15 @@ def main() -> int:
                      "binding": "valu",
                      "valu": None if insts is None else {
                          "insts_per_launch": int(insts), "unit": "G wave-instr/s",
-                         "achieved": round(insts / (kms[0] * 1e-3) / 1e9, 1),
+                         "achieved": round(insts / (kms * 1e-3) / 1e9, 1),
                          "peak": round(peak_valu / 1e9, 1),
-                         "frac": round(insts / (kms[0] * 1e-3) / peak_valu, 4)}},
+                         "frac": round(insts / (kms * 1e-3) / peak_valu, 4)}},
         "copy_peak": {"GBps": round(copy_peak_gbs, 1), "unit": "GB/s read + written",
                       "kernel": "k_copy_stream (libqs_calib.so), 1 GiB, 16-byte non-temporal "
                                 "loads and stores, 10 launches back to back"},
+        "valu_peak": {"G_wave_instr_per_s": round(peak_valu / 1e9, 1),
+                      "kernel": "k_valu_issue (libqs_calib.so), 30 launches of ~7 ms, "
+                                "before the headline"},
         "per_type": per_type,
         "configs": configs,
     }

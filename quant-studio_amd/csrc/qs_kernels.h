@@ -51,6 +51,33 @@ constexpr int Q40_TILE = 64;                   // blocks per 256-thread tile (4 
 constexpr int Q40_TILES = 4;                   // tiles per workgroup, loaded before any compute
 constexpr int Q40_BLOCKS_PER_WG = Q40_TILE * Q40_TILES;
 
+// Lane (lane ^ M) of the lane's group of four (M = 1 or 2): a DPP quad
+// permute, a VALU move with no LDS round trip (a width-4 __shfl_xor compiles
+// to ds_bpermute and a wait on LDS). Every lane of the group must be active.
+template <int M>
+QS_DEV uint32_t quad_xor(uint32_t v) {
+    static_assert(M == 1 || M == 2, "quad lanes");
+    constexpr int ctrl = M == 1 ? 0xB1 : 0x4E;     // quad_perm:[1,0,3,2] / [2,3,0,1]
+    // bound_ctrl: a quad permute never reads outside the row, so no lane keeps
+    // the (unused) old value
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, true);
+}
+template <int M>
+QS_DEV float quad_xor(float v) {
+    return __builtin_bit_cast(float, quad_xor<M>(__builtin_bit_cast(uint32_t, v)));
+}
+
+// one round of the quarters' absmax merge: take the partner's (max, value)
+// when its max is larger, or equal and the partner is the lower quarter
+template <int M>
+QS_DEV void quad_absmax_round(float& am, float& mv, int q) {
+    const float pam = quad_xor<M>(am);
+    const float pmv = quad_xor<M>(mv);
+    const bool take = (pam > am) | ((pam == am) & ((q ^ M) < q));
+    am = take ? pam : am;
+    mv = take ? pmv : mv;
+}
+
 // signed value of the largest |x| of the block, first index wins (argmax of
 // abs): the lane's max |x|, then its first value of that magnitude, then the
 // lowest quarter holding the block's max
@@ -61,14 +88,8 @@ QS_DEV float quad_absmax_first(const float (&x)[8], int q) {
     float mv = x[7];
 #pragma unroll
     for (int i = 6; i >= 0; i--) mv = fabsf(x[i]) == am ? x[i] : mv;
-#pragma unroll
-    for (int m = 1; m <= 2; m <<= 1) {
-        const float pam = __shfl_xor(am, m, 4);
-        const float pmv = __shfl_xor(mv, m, 4);
-        const bool take = pam > am || (pam == am && (q ^ m) < q);
-        am = take ? pam : am;
-        mv = take ? pmv : mv;
-    }
+    quad_absmax_round<1>(am, mv, q);
+    quad_absmax_round<2>(am, mv, q);
     return mv;
 }
 
@@ -80,25 +101,27 @@ QS_DEV void quad_min_max(const float (&x)[8], float& mn, float& mx) {
         mn = fminf(mn, x[i]);
         mx = fmaxf(mx, x[i]);
     }
-#pragma unroll
-    for (int m = 1; m <= 2; m <<= 1) {
-        mn = fminf(mn, __shfl_xor(mn, m, 4));
-        mx = fmaxf(mx, __shfl_xor(mx, m, 4));
-    }
+    mn = fminf(mn, quad_xor<1>(mn));
+    mx = fmaxf(mx, quad_xor<1>(mx));
+    mn = fminf(mn, quad_xor<2>(mn));
+    mx = fmaxf(mx, quad_xor<2>(mx));
 }
 
-// qs[j] = L[j] & 15 | (L[j+16] & 15) << 4 from the lanes' 8 nibbles: quarters
-// 0/1 hold the low halves and take the high nibbles of quarters 2/3; writes
-// 8 bytes at o (q < 2), o 2-byte aligned
-QS_DEV void quad_store_nibbles(uint32_t nib, int q, uint8_t* o) {
-    const uint32_t hi = __shfl_xor(nib, 2, 4);
-    if (q < 2) {
-        uint32_t w0 = 0, w1 = 0;
+// The lane's 8 levels (each < 256) as bytes: w[0] = L0..L3, w[1] = L4..L7
+QS_DEV void bytes_of(const uint32_t (&l)[8], uint32_t (&w)[2]) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            w0 |= (((nib >> (4 * i)) & 15u) | (((hi >> (4 * i)) & 15u) << 4)) << (8 * i);
-            w1 |= (((nib >> (4 * (i + 4))) & 15u) | (((hi >> (4 * (i + 4))) & 15u) << 4)) << (8 * i);
-        }
+    for (int h = 0; h < 2; h++)
+        w[h] = l[4 * h] | (l[4 * h + 1] << 8) | (l[4 * h + 2] << 16) | (l[4 * h + 3] << 24);
+}
+
+// qs[j] = L[j] & 15 | (L[j+16] & 15) << 4 from the lanes' level bytes:
+// quarters 0/1 hold the low halves and take the high nibbles of quarters 2/3
+// (one exchange per word); writes 8 bytes at o (q < 2), o 2-byte aligned
+QS_DEV void quad_store_nibbles(const uint32_t (&w)[2], int q, uint8_t* o) {
+    const uint32_t hi0 = quad_xor<2>(w[0]), hi1 = quad_xor<2>(w[1]);
+    if (q < 2) {
+        const uint32_t w0 = (w[0] & 0x0f0f0f0fu) | ((hi0 & 0x0f0f0f0fu) << 4);
+        const uint32_t w1 = (w[1] & 0x0f0f0f0fu) | ((hi1 & 0x0f0f0f0fu) << 4);
         uint16_t* o16 = reinterpret_cast<uint16_t*>(o + 8 * q);
         o16[0] = (uint16_t)w0;
         o16[1] = (uint16_t)(w0 >> 16);
@@ -119,23 +142,23 @@ QS_DEV void b32_block(const float (&x)[8], int q, uint8_t* o) {
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         constexpr float OFF = T == B32::Q4_0 ? 8.5f : 16.5f;
         constexpr float TOP = T == B32::Q4_0 ? 15.5f : 31.5f;
-        uint32_t nib = 0, h5 = 0;
+        uint32_t l[8], w[2], h5 = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             float t = x[i] * id;
             t = t + OFF;
             // clamp(floor(t), 0, top) == trunc(clamp(t, 0, top + 0.5)): truncation
             // is floor on [0, top + 0.5] (NaN clamps to 0 either way)
-            const uint32_t qv = (uint32_t)clampf(t, 0.0f, TOP);
-            nib |= (qv & 15u) << (4 * i);
-            h5 |= (qv >> 4) << i;
+            l[i] = (uint32_t)clampf(t, 0.0f, TOP);
+            if constexpr (T == B32::Q5_0) h5 |= (l[i] >> 4) << i;
         }
+        bytes_of(l, w);
         if (q == 0) o16[0] = (uint16_t)f16_bits(d);
         if constexpr (T == B32::Q4_0) {
-            quad_store_nibbles(nib, q, o + 2);
+            quad_store_nibbles(w, q, o + 2);
         } else {
             o[2 + q] = (uint8_t)h5;                 // qh: bit j is bit 4 of L[j]
-            quad_store_nibbles(nib, q, o + 6);
+            quad_store_nibbles(w, q, o + 6);
         }
     } else if constexpr (T == B32::Q4_1 || T == B32::Q5_1) {
         // d = (max - min) / nmax, m = min; L = min(nmax, trunc((x - min) * id + 0.5))
@@ -144,33 +167,33 @@ QS_DEV void b32_block(const float (&x)[8], int q, uint8_t* o) {
         quad_min_max(x, mn, mx);
         const float d = (mx - mn) / NMAX;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint32_t nib = 0, h5 = 0;
+        uint32_t l[8], w[2], h5 = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             float t = x[i] - mn;
             t = t * id;
             t = t + 0.5f;
-            const uint32_t qv = (uint32_t)clampf(t, 0.0f, NMAX);
-            nib |= (qv & 15u) << (4 * i);
-            h5 |= (qv >> 4) << i;
+            l[i] = (uint32_t)clampf(t, 0.0f, NMAX);
+            if constexpr (T == B32::Q5_1) h5 |= (l[i] >> 4) << i;
         }
+        bytes_of(l, w);
         if (q == 0) {
             o16[0] = (uint16_t)f16_bits(d);
             o16[1] = (uint16_t)f16_bits(mn);
         }
         if constexpr (T == B32::Q4_1) {
-            quad_store_nibbles(nib, q, o + 4);
+            quad_store_nibbles(w, q, o + 4);
         } else {
             o[4 + q] = (uint8_t)h5;
-            quad_store_nibbles(nib, q, o + 8);
+            quad_store_nibbles(w, q, o + 8);
         }
     } else {
         // Q8_0: d = amax / 127, q = round half away from zero (C roundf)
         float am = fabsf(x[0]);
 #pragma unroll
         for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
-#pragma unroll
-        for (int m = 1; m <= 2; m <<= 1) am = fmaxf(am, __shfl_xor(am, m, 4));
+        am = fmaxf(am, quad_xor<1>(am));
+        am = fmaxf(am, quad_xor<2>(am));
         const float d = am / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t w[2] = {0u, 0u};
