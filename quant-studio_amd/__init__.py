@@ -206,7 +206,9 @@ def quantize(ggml_type: int, x, qw, out=None):
     esz = x.element_size()
     if n > 0 and ((k > 1 and x.stride(1) != 1) or x.data_ptr() % 16 or
                   (n > 1 and (x.stride(0) < k or (x.stride(0) * esz) % 16))):
-        x = x.contiguous()
+        # an explicit copy: x.contiguous() returns x itself for a contiguous
+        # view that starts off a 16-byte boundary; a fresh allocation does not
+        x = torch.empty((n, k), dtype=x.dtype, device=x.device).copy_(x)
     rb = row_bytes(ggml_type, k)
     if out is None:
         out = torch.empty((n, rb), dtype=torch.uint8, device=x.device)

@@ -63,8 +63,10 @@ OPTIONS = (
            "name=ggml_type entries, whitespace-separated"),
     Option("--dry-run", "switch", False, None, "print the per-tensor plan and sizes, write nothing"),
     Option("--sqrt-rounding", "value", "torch-cpu", None,
-           "whose torch.sqrt the weights follow: torch-cpu (Intel host, default), "
-           "torch-cpu-amd (AMD EPYC host) or ieee"),
+           "whose torch.sqrt the weights follow: torch-cpu (the reference's eager CPU "
+           "path on an Intel host, default, for every --device), torch-cpu-amd (the "
+           "same on an AMD EPYC host) or ieee (correctly rounded, as the reference's "
+           "GPU path computes it); --device auto/cuda does not select ieee"),
 )
 
 # llama-quantize options the reference recognises and refuses (quant-studio.py:305-312)
@@ -394,7 +396,7 @@ def main(argv: list[str] | None = None) -> int:
     req = parse_request(argv)
     device_shown = "rocm" if req.device not in ("cpu", "mps") else f"{req.device} (on rocm)"
     print(f"quant-studio: {req.src} -> {req.dst} [{req.option.name}] device={device_shown} "
-          f"mem={req.mem_text}")
+          f"mem={req.mem_text} sqrt-rounding={req.sqrt_rounding}")
     imatrix: dict[str, np.ndarray] = {}
     if req.imatrix is not None:
         imatrix = load_imatrix(req.imatrix)

@@ -12,6 +12,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <system_error>
 #include <thread>
 #include <tuple>
 #include <utility>
@@ -205,9 +206,17 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
     const int nthr = (int)std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
     std::vector<Part> parts(nthr);
     std::vector<std::thread> threads;
-    for (int k = 0; k < nthr; k++)
-        threads.emplace_back(build_range, (int)((int64_t)ksize * k / nthr), (int)((int64_t)ksize * (k + 1) / nthr),
-                             std::ref(parts[k]));
+    int started = 0;
+    try {
+        for (; started < nthr; started++)
+            threads.emplace_back(build_range, (int)((int64_t)ksize * started / nthr),
+                                 (int)((int64_t)ksize * (started + 1) / nthr), std::ref(parts[started]));
+    } catch (const std::system_error&) {
+        // no more threads (a process limit, a sandbox): this thread builds the
+        // remaining ranges; the ranges and their join are the same either way
+    }
+    for (int k = started; k < nthr; k++)
+        build_range((int)((int64_t)ksize * k / nthr), (int)((int64_t)ksize * (k + 1) / nthr), parts[k]);
     for (auto& th : threads) th.join();
     // join the ranges in code order, moving each range's starts by the lists before it
     size_t base = 0;

@@ -140,6 +140,17 @@ def test_cpu_and_mps_devices_are_accepted(tmp_path):
         assert f"device={dev} (on rocm)" in r.stdout and "dry run:" in r.stdout
 
 
+def test_header_names_the_square_root_rounding(tmp_path):
+    """The header line shows whose torch.sqrt rounding the weights follow, for
+    the default and a chosen mode (--device does not change it)."""
+    src = tmp_path / "in.gguf"
+    small_model(src, odd=False)
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--dry-run")
+    assert "sqrt-rounding=torch-cpu" in r.stdout.splitlines()[0]
+    r = run_cli(src, tmp_path / "o.gguf", "q4_0", "--device", "cuda", "--sqrt-rounding", "ieee", "--dry-run")
+    assert "sqrt-rounding=ieee" in r.stdout.splitlines()[0]
+
+
 def test_mem_and_size_helpers():
     cli = importlib.import_module("quant-studio_amd.cli")
     assert cli.parse_mem("4G") == 4 << 30 and cli.parse_mem(" 512m ") == 512 << 20

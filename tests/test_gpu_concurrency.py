@@ -44,12 +44,13 @@ def work(t):
         with torch.cuda.stream(s):
             x, q = xb.to(dev, non_blocking=False), torch.from_numpy(qw).to(dev)
             s.synchronize()
-            start.wait()
+            start.wait(timeout=120)
             outs = [qs.quantize(TYPES[t][0], x, q) for _ in range(3)]
             s.synchronize()
         results[t] = [o.cpu().numpy() for o in outs]
     except Exception as e:
         errors.append(f"{t}: {e!r}")
+        start.abort()          # release the threads waiting at the barrier
 
 threads = [threading.Thread(target=work, args=(t,)) for t in types]
 for th in threads:

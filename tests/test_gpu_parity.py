@@ -298,16 +298,22 @@ def test_cpu_device_quant_fn(qs, dev, qtype):
 
 def test_layouts_the_c_call_refuses_are_copied(qs, dev):
     """Views the C call does not take (column offset not 16-byte aligned, row
-    stride not a multiple of 16 bytes, an expanded row) are quantized from a
-    contiguous copy: same bytes as the contiguous tensor."""
+    stride not a multiple of 16 bytes, a contiguous view starting off a
+    16-byte boundary, an expanded row) are quantized from a contiguous copy:
+    same bytes as the contiguous tensor."""
     x, qw = ffn_like(24, 512, seed=8)
     base = torch.zeros((24, 512 + 40), dtype=torch.bfloat16, device=dev)
     base[:, 1:513] = to_device(x, dev)
     odd = torch.zeros((24, 516), dtype=torch.bfloat16, device=dev)
     odd[:, :512] = to_device(x, dev)
     q = torch.from_numpy(qw).to(dev)
+    flat = torch.zeros(24 * 512 + 8, dtype=torch.bfloat16, device=dev)
+    flat[1:1 + 24 * 512] = to_device(x, dev).reshape(-1)
+    shifted = flat[1:1 + 24 * 512].view(24, 512)
+    assert shifted.is_contiguous() and shifted.data_ptr() % 16 == 2
     views = {"column offset 1 (2 bytes)": base[:, 1:513],
-             "row stride 1032 bytes": odd[:, :512]}
+             "row stride 1032 bytes": odd[:, :512],
+             "contiguous view 2 bytes past a 16-byte boundary": shifted}
     for qtype in ("q4_0", "q4_k", "iq3_xxs"):
         tid = TYPES[qtype][0]
         ref = oracle.quantize(qtype, x, None if qtype == "q4_0" else qw, n_threads=NTHREADS)
