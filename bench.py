@@ -30,6 +30,7 @@ The JSON line also carries:
 usage: python bench.py [--gpus 1] [--steps 100] [--warmup 300] [--types all|none|q4_k,...]
        python bench.py --e2e 'IQ2_XXS;Q4_K_M'   the command line end to end on a
                                                synthetic 4B-class model (warm and cold)
+       python bench.py --e2e all               the same for the reference's published runs
 """
 
 from __future__ import annotations
@@ -529,6 +530,20 @@ def drop_page_cache(path: Path) -> None:
         os.close(fd)
 
 
+# The reference's published end-to-end runs on a 4B bf16 model (README.md:28-49:
+# every scheme with one imatrix, Q4_0 without; README.md:62-64: three --pure
+# runs). A "--no-imatrix" token (bench.py's, not the command line's) runs
+# the scheme without the imatrix.
+E2E_PUBLISHED = ["IQ2_XXS", "IQ2_XS", "IQ2_S", "IQ2_M", "Q2_K_S", "Q2_K", "IQ3_XXS", "IQ3_XS",
+                 "IQ3_S", "IQ3_M", "Q3_K_S", "Q3_K_M", "Q3_K_L", "IQ4_XS", "Q4_0 --no-imatrix",
+                 "Q4_K_S", "Q4_K_M", "Q5_K_S", "Q5_K_M", "Q6_K",
+                 "Q4_0 --pure --no-imatrix", "Q4_K --pure", "IQ2_XXS --pure"]
+# the default run's end-to-end leg: the full-model IQ2_XXS run, the Q4_K_M mix
+# with --mem 4G, and the IQ3_XXS and IQ2_S schemes with a Q4_0 token embedding
+E2E_DEFAULT = ["IQ2_XXS", "Q4_K_M --mem 4G", "IQ3_XXS --token-embedding-type q4_0",
+               "IQ2_S --token-embedding-type q4_0"]
+
+
 def e2e_runs(torch, dev, schemes: list[str], where: str | None) -> dict:
     """The command line on the synthetic model, per scheme: one run with the
     input in the page cache (warm) and one after evicting the input and the
@@ -550,13 +565,15 @@ def e2e_runs(torch, dev, schemes: list[str], where: str | None) -> dict:
         results = {}
         for sch in schemes:
             name, *extra = sch.split()
+            use_im = "--no-imatrix" not in extra
+            extra = [a for a in extra if a != "--no-imatrix"]
             for cache in ("warm", "cold"):
                 out = d / f"out-{name}.gguf"
                 if cache == "cold":
                     drop_page_cache(src)
                     drop_page_cache(im)
                 cmd = [sys.executable, str(ROOT / "quant-studio.py"), str(src), str(out), name,
-                       "--imatrix", str(im), *extra]
+                       *(["--imatrix", str(im)] if use_im else []), *extra]
                 t0 = time.perf_counter()
                 r = subprocess.run(cmd, capture_output=True, text=True)
                 wall = time.perf_counter() - t0
@@ -603,10 +620,12 @@ def main() -> int:
                     help="square-root rounding of the weights (the oracle follows it)")
     ap.add_argument("--e2e", default=None,
                     help="run the CLI end to end on a synthetic 4B-class model for these "
-                         "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M') and print its own JSON line")
+                         "';'-separated schemes (e.g. 'IQ2_XXS;Q4_K_M'), or 'all' for the "
+                         "reference's published runs, and print its own JSON line")
     ap.add_argument("--no-e2e", action="store_true",
                     help="skip the default end-to-end leg (the command line on the synthetic "
-                         "4B-class model, IQ2_XXS warm and cold)")
+                         "4B-class model: IQ2_XXS, Q4_K_M --mem 4G, IQ3_XXS and IQ2_S with a "
+                         "Q4_0 token embedding; warm and cold)")
     ap.add_argument("--e2e-dir", default=None, help="directory for the e2e model (default: the "
                     "first disk-backed of $TMPDIR, /tmp, /var/tmp, the repository)")
     ap.add_argument("--valu-peak", action="store_true",
@@ -631,7 +650,9 @@ def main() -> int:
         print(json.dumps({"valu_wave_instr_per_s": round(valu_peak(torch, dev, args.steps))}), flush=True)
         return 0
     if args.e2e:
-        return run_e2e(torch, dev, [x.strip() for x in args.e2e.split(";") if x.strip()], args.e2e_dir)
+        schemes = E2E_PUBLISHED if args.e2e == "all" else \
+            [x.strip() for x in args.e2e.split(";") if x.strip()]
+        return run_e2e(torch, dev, schemes, args.e2e_dir)
     qs.set_sqrt_rounding(args.sqrt)
     qs.init(0)
     xs, qws, host = make_inputs(torch, dev)
@@ -782,12 +803,11 @@ def main() -> int:
         head = cb["per_type"].get("q4_k+imat")
         line["identical_pct_vs_oracle"] = None if head is None else head["identical_pct"]
     if not args.no_e2e:
-        # the command line end to end on the synthetic 4B-class model (the
-        # Q4_K_M mix with --mem 4G and the full-model IQ2_XXS run), warm and
-        # cold page cache;
-        # supplementary to the headline, so a failure is reported in the line
+        # the command line end to end on the synthetic 4B-class model
+        # (E2E_DEFAULT), warm and cold page cache; supplementary to the
+        # headline, so a failure is reported in the line
         try:
-            line["e2e"] = e2e_runs(torch, dev, ["IQ2_XXS", "Q4_K_M --mem 4G"], args.e2e_dir)
+            line["e2e"] = e2e_runs(torch, dev, E2E_DEFAULT, args.e2e_dir)
         except Exception as e:
             print(f"bench: e2e leg failed: {e}", file=sys.stderr, flush=True)
             line["e2e"] = {"error": str(e)[-500:]}

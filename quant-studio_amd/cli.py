@@ -332,6 +332,23 @@ def device_index(req: Request, ndev: int) -> int:
     return index
 
 
+def preallocate(fd: int, size: int) -> bool:
+    """Allocate the output file's blocks up front with the fallocate(2) system
+    call: writes into the page cache then skip ext4's per-page delayed
+    allocation (about twice the pwrite rate there). Where the filesystem
+    cannot (EOPNOTSUPP) nothing happens and the writes allocate as usual; glibc's
+    posix_fallocate would instead write a byte into every block."""
+    import ctypes
+    try:
+        libc = ctypes.CDLL(None, use_errno=True)
+        fn = libc.fallocate
+    except (OSError, AttributeError):
+        return False
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    fn.restype = ctypes.c_int
+    return size > 0 and fn(fd, 0, 0, size) == 0
+
+
 def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: dict) -> None:
     from . import library, row_bytes, SQRT_ROUNDING
     from .pipeline import NativePipeline, PipelineError, Readahead, device_count
@@ -358,6 +375,7 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
     base = writer.data_start()
     writer.fout.flush()
     fd = writer.fout.fileno()
+    preallocate(fd, writer.total_size())
 
     total_in = total_out = 0
     t0 = time.time()

@@ -3,9 +3,11 @@
 //
 // Replaces the reference's CudaPipeline (quant-studio.py:148-213),
 // OutputWriter (:103-131) and copy_tensor (:235-241):
-//   - a ring of slots (pinned in/out, device in/out/imatrix), so the host copy
-//     of chunk i+2, the H2D of chunk i+1, the kernel of chunk i and the D2H
-//     and file write of chunk i-1 overlap;
+//   - a ring of input slots (pinned rows and imatrix, their device copies) and
+//     a deeper ring of output slots (device output, pinned copy), so the host
+//     copy of chunk i+2, the H2D of chunk i+1, the kernel of chunk i and the
+//     D2H and file write of earlier chunks overlap, and a writer a few chunks
+//     behind does not hold back the next uploads;
 //   - the mapping -> pinned copy of a chunk split over a pool of threads (one
 //     thread caps the pipeline well below the PCIe rate);
 //   - H2D and D2H on two copy streams (so the next chunk's upload never queues
@@ -216,12 +218,24 @@ struct DevBuf {
     }
 };
 
-struct Slot {
-    PinnedBuf in_pin, out_pin, qw_pin;
-    DevBuf x_dev, out_dev, qw_dev;
-    hipEvent_t h2d = nullptr, kern = nullptr, d2h = nullptr;
-    bool used = false;        // events recorded at least once
-    uint64_t write_seq = 0;   // writer job that reads out_pin
+// Input ring: pinned staging of the rows, their device copy and the imatrix.
+struct InSlot {
+    PinnedBuf in_pin, qw_pin;
+    DevBuf x_dev, qw_dev;
+    hipEvent_t h2d = nullptr;     // the rows (and imatrix) are on the device
+    hipEvent_t kern = nullptr;    // the kernel that read x_dev / qw_dev is done
+    bool used = false;            // events recorded at least once
+};
+
+// Output ring: the kernel's device output and its pinned copy for the writer.
+// Deeper than the input ring, so a writer running a few chunks behind the GPU
+// does not stop the calling thread from staging the next inputs.
+struct OutSlot {
+    DevBuf out_dev;
+    PinnedBuf out_pin;
+    hipEvent_t d2h = nullptr;     // out_pin holds the chunk; out_dev is free
+    bool used = false;
+    uint64_t write_seq = 0;       // writer job that reads out_pin
 };
 
 int elem_size(int src_type) {
@@ -238,8 +252,9 @@ int elem_size(int src_type) {
 struct qs_pipeline {
     int device = 0;
     hipStream_t h2d = nullptr, d2h = nullptr, compute[2] = {nullptr, nullptr};
-    std::vector<Slot> slots;
-    size_t next = 0;
+    std::vector<InSlot> in_slots;
+    std::vector<OutSlot> out_slots;
+    size_t next_in = 0, next_out = 0;
     uint64_t launches = 0;    // picks the compute stream of the next kernel
     std::unique_ptr<CopyPool> pool;
     std::unique_ptr<Writer> writer;
@@ -284,11 +299,17 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline*
         qs_pipeline_destroy(p.release());
         return fail(QS_EIO, "stream creation failed: %s", hipGetErrorString(e));
     }
-    p->slots.resize(n_slots);
-    for (auto& s : p->slots) {
+    p->in_slots.resize(n_slots);
+    p->out_slots.resize(std::max(8, 2 * n_slots));
+    for (auto& s : p->in_slots) {
         if ((e = hipEventCreateWithFlags(&s.h2d, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&s.kern, hipEventDisableTiming)) != hipSuccess ||
-            (e = hipEventCreateWithFlags(&s.d2h, hipEventDisableTiming)) != hipSuccess) {
+            (e = hipEventCreateWithFlags(&s.kern, hipEventDisableTiming)) != hipSuccess) {
+            qs_pipeline_destroy(p.release());
+            return fail(QS_EIO, "event creation failed: %s", hipGetErrorString(e));
+        }
+    }
+    for (auto& s : p->out_slots) {
+        if ((e = hipEventCreateWithFlags(&s.d2h, hipEventDisableTiming)) != hipSuccess) {
             qs_pipeline_destroy(p.release());
             return fail(QS_EIO, "event creation failed: %s", hipGetErrorString(e));
         }
@@ -332,27 +353,33 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
     for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_chunk) {
         const int64_t n = std::min(rows_per_chunk, n_rows - r0);
         const size_t nin = (size_t)(n * in_row), nout = (size_t)(n * out_row), nqw = use_qw ? (size_t)k * 4 : 0;
-        Slot& s = p->slots[p->next];
-        p->next = (p->next + 1) % p->slots.size();
-        if (s.used) {
-            // in_pin: its H2D is done; out_pin: its write is done; device
-            // buffers: the kernel and the D2H that used them are done
-            if ((e = hipEventSynchronize(s.h2d)) != hipSuccess) return p->hip_fail(e, "H2D");
-            p->writer->wait(s.write_seq);
-            if (int rc = p->check_writer()) return rc;
-            if (s.x_dev.n < nin || s.out_dev.n < nout || s.qw_dev.n < nqw) {
-                if ((e = hipEventSynchronize(s.d2h)) != hipSuccess) return p->hip_fail(e, "D2H");
-            }
+        InSlot& si = p->in_slots[p->next_in];
+        OutSlot& so = p->out_slots[p->next_out];
+        p->next_in = (p->next_in + 1) % p->in_slots.size();
+        p->next_out = (p->next_out + 1) % p->out_slots.size();
+        if (si.used) {
+            // in_pin: its H2D is done; the device buffers: if they must grow,
+            // the kernel that read them is done
+            if ((e = hipEventSynchronize(si.h2d)) != hipSuccess) return p->hip_fail(e, "H2D");
+            if ((si.x_dev.n < nin || si.qw_dev.n < nqw) && (e = hipEventSynchronize(si.kern)) != hipSuccess)
+                return p->hip_fail(e, "kernel");
         }
-        if (!s.in_pin.grow(nin) || !s.out_pin.grow(nout) || !s.qw_pin.grow(nqw) || !s.x_dev.grow(nin) ||
-            !s.out_dev.grow(nout) || !s.qw_dev.grow(nqw)) {
+        if (so.used) {
+            // out_pin: its write is done; out_dev: if it must grow, its D2H is done
+            p->writer->wait(so.write_seq);
+            if (int rc = p->check_writer()) return rc;
+            if (so.out_dev.n < nout && (e = hipEventSynchronize(so.d2h)) != hipSuccess)
+                return p->hip_fail(e, "D2H");
+        }
+        if (!si.in_pin.grow(nin) || !si.qw_pin.grow(nqw) || !si.x_dev.grow(nin) || !si.qw_dev.grow(nqw) ||
+            !so.out_pin.grow(nout) || !so.out_dev.grow(nout)) {
             if (p->err.empty()) p->err = "out of memory staging a chunk";
             return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)n,
                         (long long)in_row);
         }
         // mapping -> pinned, in parts of at least kCopyPart bytes
         const char* from = rows + r0 * in_row;
-        char* to = static_cast<char*>(s.in_pin.p);
+        char* to = static_cast<char*>(si.in_pin.p);
         const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), nin / kCopyPart));
         std::vector<std::function<void()>> tasks;
         for (size_t i = 0; i < parts; i++) {
@@ -360,31 +387,33 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
             tasks.emplace_back([=] { std::memcpy(to + a, from + a, b - a); });
         }
         p->pool->run(tasks);
-        if (nqw) std::memcpy(s.qw_pin.p, imatrix, nqw);
+        if (nqw) std::memcpy(si.qw_pin.p, imatrix, nqw);
 
-        if (s.used && (e = hipStreamWaitEvent(p->h2d, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(s.x_dev.p, s.in_pin.p, nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
+        // the upload overwrites x_dev / qw_dev once the kernel that read them is done
+        if (si.used && (e = hipStreamWaitEvent(p->h2d, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(si.x_dev.p, si.in_pin.p, nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
             return p->hip_fail(e, "H2D");
-        if (nqw && (e = hipMemcpyAsync(s.qw_dev.p, s.qw_pin.p, nqw, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
+        if (nqw && (e = hipMemcpyAsync(si.qw_dev.p, si.qw_pin.p, nqw, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
             return p->hip_fail(e, "H2D");
-        if ((e = hipEventRecord(s.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipEventRecord(si.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
+        // the kernel writes out_dev once the D2H that read it is done
         hipStream_t cs = p->compute[p->launches++ & 1];
-        if ((e = hipStreamWaitEvent(cs, s.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if (s.used && (e = hipStreamWaitEvent(cs, s.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        const int rc = qs_quantize(ggml_type, src_type, s.x_dev.p, n, k, in_row,
-                                   nqw ? static_cast<const float*>(s.qw_dev.p) : nullptr, s.out_dev.p,
+        if ((e = hipStreamWaitEvent(cs, si.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if (so.used && (e = hipStreamWaitEvent(cs, so.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        const int rc = qs_quantize(ggml_type, src_type, si.x_dev.p, n, k, in_row,
+                                   nqw ? static_cast<const float*>(si.qw_dev.p) : nullptr, so.out_dev.p,
                                    (int64_t)nout, cs);
         if (rc) {
             if (p->err.empty()) p->err = "quantizer launch failed";
             return rc;
         }
-        if ((e = hipEventRecord(s.kern, cs)) != hipSuccess) return p->hip_fail(e, "event");
-        if ((e = hipStreamWaitEvent(p->d2h, s.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(s.out_pin.p, s.out_dev.p, nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
+        if ((e = hipEventRecord(si.kern, cs)) != hipSuccess) return p->hip_fail(e, "event");
+        if ((e = hipStreamWaitEvent(p->d2h, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+        if ((e = hipMemcpyAsync(so.out_pin.p, so.out_dev.p, nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
             return p->hip_fail(e, "D2H");
-        if ((e = hipEventRecord(s.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
-        s.used = true;
-        s.write_seq = p->writer->push({s.d2h, s.out_pin.p, nout, fd, out_offset + r0 * out_row});
+        if ((e = hipEventRecord(so.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
+        si.used = so.used = true;
+        so.write_seq = p->writer->push({so.d2h, so.out_pin.p, nout, fd, out_offset + r0 * out_row});
     }
     return 0;
 }
@@ -423,15 +452,17 @@ void qs_pipeline_destroy(qs_pipeline* p) {
         if (cs) (void)hipStreamSynchronize(cs);
     p->writer.reset();
     p->pool.reset();
-    for (auto& s : p->slots) {
+    for (auto& s : p->in_slots) {
         s.in_pin.release();
-        s.out_pin.release();
         s.qw_pin.release();
         s.x_dev.release();
-        s.out_dev.release();
         s.qw_dev.release();
         if (s.h2d) (void)hipEventDestroy(s.h2d);
         if (s.kern) (void)hipEventDestroy(s.kern);
+    }
+    for (auto& s : p->out_slots) {
+        s.out_pin.release();
+        s.out_dev.release();
         if (s.d2h) (void)hipEventDestroy(s.d2h);
     }
     if (p->h2d) (void)hipStreamDestroy(p->h2d);

@@ -275,3 +275,25 @@ def test_readahead_walks_the_plan_within_its_budget(tmp_path):
         assert win[0][0] == a0 - a0 % page and all(n == 1 << 18 for _, n in win[:-1])
         assert sum(n for _, n in win) == (1 << 20) + a0 % page
         assert all(win[i + 1][0] == win[i][0] + win[i][1] for i in range(len(win) - 1))
+
+
+def test_preallocate_keeps_written_bytes(tmp_path):
+    """The output file's blocks are allocated up front (fallocate(2)); bytes
+    already written stay, the size becomes the planned one, and a descriptor
+    that cannot be extended reports False instead of raising."""
+    import os
+    cli = importlib.import_module("quant-studio_amd.cli")
+    path = tmp_path / "o.bin"
+    fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        os.write(fd, b"GGUF-header")
+        assert cli.preallocate(fd, 1 << 20)
+        assert os.fstat(fd).st_size == 1 << 20
+    finally:
+        os.close(fd)
+    assert path.read_bytes()[:11] == b"GGUF-header"
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        assert not cli.preallocate(fd, 2 << 20)
+    finally:
+        os.close(fd)
