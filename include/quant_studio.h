@@ -163,9 +163,11 @@ typedef struct qs_pipeline qs_pipeline;
  * quant-studio.py:51-58). */
 int qs_device_count(void);
 
-/* Pipeline on `device` with n_slots chunk slots (2..16; 3 keeps host copy,
- * H2D, kernel and D2H+write of consecutive chunks overlapped) and
- * n_copy_threads host threads (1..64) for the mapping -> pinned copies. */
+/* Pipeline on `device` with n_slots input slots (2..16; 3 keeps the host
+ * copy, H2D and kernel of consecutive chunks overlapped), max(8, 2 n_slots)
+ * output slots (device output and its pinned copy, so a writer a few chunks
+ * behind does not hold back the next uploads), and n_copy_threads host
+ * threads (1..64) for the mapping -> pinned copies. */
 int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline **out);
 
 /* Queue one tensor: n_rows rows of k values of src_type at host address src
