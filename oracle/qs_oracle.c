@@ -234,6 +234,25 @@ static float sum_seq(const float *v, int n) {
     return s;
 }
 
+/* Magnitude of v as an ordered key: the float order for finite and infinite
+ * values, every NaN one above Inf and equal to every other NaN. torch's
+ * argmax of |x| (q4_0.py:21-22) takes the first NaN as the maximum. */
+static uint32_t mag_key(float v) {
+    uint32_t b;
+    memcpy(&b, &v, sizeof b);
+    b &= 0x7fffffffu;
+    return b < 0x7f800001u ? b : 0x7f800001u;
+}
+
+/* the first index of the largest magnitude, a NaN above everything */
+static int argmax_abs_nan(const float *b, int n) {
+    int im = 0;
+    uint32_t am = mag_key(b[0]);
+    for (int i = 1; i < n; i++)
+        if (mag_key(b[i]) > am) { am = mag_key(b[i]); im = i; }
+    return im;
+}
+
 /* absmax_first qx_common.py:26-34: value with the largest |x|, first index wins */
 static int absmax_first(const float *x, int n, float *amax) {
     int im = 0;
@@ -503,10 +522,7 @@ static float sumsq_c8(const float *x, int n) {
 /* Q4_0  q4_0.py:14-33                                                 */
 /* ------------------------------------------------------------------ */
 static void q4_0_block(const float *b, uint8_t *out) {
-    int im = 0;
-    float am = fabsf(b[0]);
-    for (int i = 1; i < 32; i++)
-        if (fabsf(b[i]) > am) { am = fabsf(b[i]); im = i; }
+    const int im = argmax_abs_nan(b, 32);          /* b.abs().argmax() q4_0.py:21 */
     float d = b[im] / -8.0f;
     float id = d != 0 ? 1.0f / d : 0.0f;
     uint8_t q[32];
@@ -853,8 +869,9 @@ static inline float DIV_N(float a, float n) { return g_mut == MUT_D_BY_RECIP ? a
 static inline float MUL_ID(float x, float id, float d) { return g_mut == MUT_X_DIV_D && d != 0 ? x / d : x * id; }
 
 static void q8_0_block(const float *b, uint8_t *out) {
-    float am = 0.0f;
-    for (int i = 0; i < 32; i++) am = fmaxf(am, fabsf(b[i]));
+    /* fmaxf from the first value: a NaN is passed over unless every value is one */
+    float am = fabsf(b[0]);
+    for (int i = 1; i < 32; i++) am = fmaxf(am, fabsf(b[i]));
     float d = DIV_N(am, 127.0f);
     float id = d != 0 ? 1.0f / d : 0.0f;
     put_f16(out, d);
@@ -894,10 +911,7 @@ static void q_1_block(const float *b, uint8_t *out, int nmax) {
 }
 
 static void q5_0_block(const float *b, uint8_t *out) {
-    int im = 0;
-    float am = fabsf(b[0]);
-    for (int i = 1; i < 32; i++)
-        if (fabsf(b[i]) > am) { am = fabsf(b[i]); im = i; }
+    const int im = argmax_abs_nan(b, 32);          /* as Q4_0 */
     float d = b[im] / -16.0f;
     float id = d != 0 ? 1.0f / d : 0.0f;
     uint8_t q[32];

@@ -67,11 +67,19 @@ QS_DEV float quad_xor(float v) {
     return __builtin_bit_cast(float, quad_xor<M>(__builtin_bit_cast(uint32_t, v)));
 }
 
+// Magnitude of v as an ordered key: the float order for finite and infinite
+// values, every NaN one above Inf and equal to every other NaN, so the first
+// NaN of a block is its maximum, as torch's argmax of |x| takes it
+// (q4_0.py:21-22)
+QS_DEV uint32_t mag_key(float v) {
+    return min(__float_as_uint(v) & 0x7fffffffu, 0x7f800001u);
+}
+
 // one round of the quarters' absmax merge: take the partner's (max, value)
 // when its max is larger, or equal and the partner is the lower quarter
 template <int M>
-QS_DEV void quad_absmax_round(float& am, float& mv, int q) {
-    const float pam = quad_xor<M>(am);
+QS_DEV void quad_absmax_round(uint32_t& am, float& mv, int q) {
+    const uint32_t pam = quad_xor<M>(am);
     const float pmv = quad_xor<M>(mv);
     const bool take = (pam > am) | ((pam == am) & ((q ^ M) < q));
     am = take ? pam : am;
@@ -79,15 +87,18 @@ QS_DEV void quad_absmax_round(float& am, float& mv, int q) {
 }
 
 // signed value of the largest |x| of the block, first index wins (argmax of
-// abs): the lane's max |x|, then its first value of that magnitude, then the
-// lowest quarter holding the block's max
+// abs, a NaN above everything): the lane's max key, then its first value of
+// that key, then the lowest quarter holding the block's max
 QS_DEV float quad_absmax_first(const float (&x)[8], int q) {
-    float am = fabsf(x[0]);
+    uint32_t key[8];
 #pragma unroll
-    for (int i = 1; i < 8; i++) am = fmaxf(am, fabsf(x[i]));
+    for (int i = 0; i < 8; i++) key[i] = mag_key(x[i]);
+    uint32_t am = key[0];
+#pragma unroll
+    for (int i = 1; i < 8; i++) am = max(am, key[i]);
     float mv = x[7];
 #pragma unroll
-    for (int i = 6; i >= 0; i--) mv = fabsf(x[i]) == am ? x[i] : mv;
+    for (int i = 6; i >= 0; i--) mv = key[i] == am ? x[i] : mv;
     quad_absmax_round<1>(am, mv, q);
     quad_absmax_round<2>(am, mv, q);
     return mv;

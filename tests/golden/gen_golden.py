@@ -196,6 +196,55 @@ def make_zero_cases() -> dict[str, dict[str, np.ndarray]]:
     return cases
 
 
+def make_nonfinite_cases() -> dict[str, dict[str, np.ndarray]]:
+    """Rows holding NaN and +-Inf among ordinary values: one value per block,
+    a whole block, the first and the last value of a 32/256-value group."""
+    rng = np.random.default_rng(20261203)
+    k = 512
+    a = rng.standard_normal((12, k)) * 0.02
+    a[0, 5] = np.nan
+    a[1, 5] = np.inf
+    a[2, 5] = -np.inf
+    a[3, :32] = np.nan
+    a[4, 0] = np.nan
+    a[5, 255] = np.inf
+    a[6, 31] = -np.inf
+    a[7, 100:104] = [np.nan, np.inf, -np.inf, np.nan]
+    a[8, ::64] = np.nan
+    a[9, 300] = 1e38
+    a[10, 7] = -1e38
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    return {"nonfinite": dict(x=a.astype(np.float32), imat=qw)}
+
+
+def write_nonfinite(out: Path, only) -> None:
+    """nonfinite.npz: make_nonfinite_cases and the reference's bytes for every
+    type and imatrix mode (keys <case>.x, <case>.imat, <type>.<case>.<mode>);
+    a type whose quantizer raises on the input is left out."""
+    import importlib
+    cases = make_nonfinite_cases()
+    rec = {}
+    for cname, c in cases.items():
+        rec[f"{cname}.x"] = c["x"]
+        rec[f"{cname}.imat"] = c["imat"]
+    for tname, mod, fn, modes in TYPES:
+        if only and tname not in only:
+            continue
+        f = getattr(importlib.import_module(f"kernels.{mod}"), fn)
+        for cname, c in cases.items():
+            for mode in modes:
+                x = torch.from_numpy(c["x"].copy())
+                qw = torch.from_numpy(c["imat"].copy()) if mode == "imat" else None
+                try:
+                    y = f(x) if tname == "q4_0" else f(x, qw)
+                except Exception as e:          # recorded as absent
+                    print(f"{tname} {mode}: {type(e).__name__}: {e}", flush=True)
+                    continue
+                rec[f"{tname}.{cname}.{mode}"] = y.numpy().astype(np.uint8)
+        print(f"{tname}: non-finite cases written", flush=True)
+    np.savez_compressed(out / "nonfinite.npz", **rec)
+
+
 def write_zero_imatrix(out: Path, only) -> None:
     """zero_imat.npz: the cases of make_zero_cases and the reference's bytes for
     every type that uses an imatrix (keys <case>.x, <case>.imat, <type>.<case>)."""
@@ -228,6 +277,8 @@ def main() -> None:
     ap.add_argument("--only", nargs="*", help="write only these types' files (inputs.npz is left as is)")
     ap.add_argument("--zero-imatrix", action="store_true",
                     help="write only zero_imat.npz (imatrix vectors with zero entries)")
+    ap.add_argument("--nonfinite", action="store_true",
+                    help="write only nonfinite.npz (rows holding NaN and +-Inf)")
     args = ap.parse_args()
 
     install_enum_module()
@@ -237,6 +288,9 @@ def main() -> None:
     torch.set_num_threads(1)
     if args.zero_imatrix:
         write_zero_imatrix(Path(args.out), args.only)
+        return
+    if args.nonfinite:
+        write_nonfinite(Path(args.out), args.only)
         return
     cases = make_cases()
     inputs = {}

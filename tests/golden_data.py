@@ -68,3 +68,20 @@ def zero_imatrix_cases(qtype: str):
         if t == qtype:
             out.append((case, _zero[f"{case}.x"], _zero[f"{case}.imat"], _zero[key]))
     return out
+
+
+def nonfinite_case():
+    """(x f32 with NaN / +-Inf / +-1e38 values, imatrix, {"<type>.<mode>": the
+    reference's bytes}) from nonfinite.npz (gen_golden.py --nonfinite); types
+    whose reference quantizer raised on the input (Q3_K, Q6_K, IQ2_XXS) have
+    no entry."""
+    z = np.load(GOLDEN / "nonfinite.npz")
+    ref = {k.split(".", 1)[0] + "." + k.rsplit(".", 1)[1]: z[k] for k in z.files if k.count(".") == 2}
+    return z["nonfinite.x"], z["nonfinite.imat"], ref
+
+
+def clean_blocks(x: np.ndarray, block: int, limit: float = 1e18) -> np.ndarray:
+    """Per output block (row-major), True where every value is finite and small
+    enough that its square stays finite in f32."""
+    xb = x.reshape(x.shape[0], -1, block)
+    return (np.isfinite(xb) & (np.abs(xb) < limit)).all(-1).reshape(-1)

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 import oracle
-from golden_data import TYPES, block_identical, cases, zero_imatrix_cases
+from golden_data import TYPES, block_identical, cases, nonfinite_case, zero_imatrix_cases
 
 pytestmark = pytest.mark.gpu
 
@@ -96,6 +96,45 @@ def test_zero_imatrix_sqrt_modes(qs, dev, mode, qtype):
         qs.set_sqrt_rounding("torch-cpu")
         oracle.use_ieee_sqrt(False)
         oracle.use_sqrt_table(None)
+
+
+EXTRA_TYPES = {"q4_1": 3, "q5_0": 6, "q5_1": 7, "q8_0": 8, "iq4_nl": 20}
+
+
+# NaN bit patterns the hardware makes: an IQ4_XS / IQ3_S scale derived from a
+# NaN the arithmetic created carries the sign of that default NaN (positive on
+# the GPU, negative on x86), so their non-finite blocks are not compared
+NAN_SIGN_TYPES = {"iq4_xs", "iq3_s"}
+
+
+@pytest.mark.parametrize("qtype", HIP_TYPES + sorted(EXTRA_TYPES))
+def test_nonfinite_inputs_match_the_oracle(qs, dev, qtype):
+    """Rows holding NaN, +-Inf and +-1e38 values (f32 source), with and without
+    imatrix: every kernel stays in bounds and returns the oracle's bytes on
+    every block whose values are finite and below 1e18, and on every block for
+    the types whose non-finite arithmetic the oracle shares (all but IQ4_XS and
+    IQ3_S); Q4_0's bytes are then the reference's on every block
+    (test_oracle.py pins the oracle's)."""
+    from golden_data import clean_blocks
+    x, qw, ref = nonfinite_case()
+    tid = TYPES[qtype][0] if qtype in TYPES else EXTRA_TYPES[qtype]
+    bs = 32 if qtype in ("q4_0", "iq4_nl") or qtype in EXTRA_TYPES else 256
+    nb = TYPES[qtype][2] if qtype in TYPES else qs.row_bytes(tid, bs)
+    clean = clean_blocks(x, bs)
+    for imat in (False, True):
+        if qtype in NEEDS_IMATRIX and not imat:
+            continue
+        q = qw if imat else None
+        print(f"{qtype} imat={imat} non-finite rows", flush=True)
+        got = qs.quantize(tid, to_device(x, dev), None if q is None else torch.from_numpy(q).to(dev))
+        got = got.cpu().numpy()
+        want = oracle.quantize(qtype, x, q, n_threads=NTHREADS)
+        same = (got.reshape(-1, nb) == want.reshape(-1, nb)).all(1)
+        assert same[clean].all(), f"{qtype} imat={imat}: finite blocks differ from the oracle"
+        if qtype not in NAN_SIGN_TYPES:
+            assert same.all(), f"{qtype} imat={imat}: non-finite blocks differ from the oracle"
+        if qtype == "q4_0":
+            assert np.array_equal(got, ref["q4_0.none"]), "q4_0: differs from the reference"
 
 
 def ffn_like(rows: int, k: int, seed: int):

@@ -17,7 +17,8 @@ import pytest
 import torch
 
 import oracle
-from golden_data import ORACLE_TYPES, block_identical, cases, zero_imatrix_cases
+from golden_data import (ORACLE_TYPES, TYPES, block_identical, cases, clean_blocks, nonfinite_case,
+                         zero_imatrix_cases)
 
 
 @pytest.mark.parametrize("qtype", ORACLE_TYPES)
@@ -77,6 +78,32 @@ def test_zero_imatrix_vectors_catch_planted_mistake(mut):
                 f"planted mistake '{what}' not detected by {qtype} {case}"
     finally:
         L.qso_set_mutation(0)
+
+
+def test_nonfinite_inputs_match_the_reference_on_every_finite_block():
+    """Rows holding NaN, +-Inf and +-1e38 (whose squares overflow): the
+    reference's quantizers raise on them for Q3_K, Q6_K and IQ2_XXS and
+    otherwise follow torch's NaN propagation (argmax takes a NaN as the
+    maximum), which the oracle and the kernels do not reproduce. Every block
+    whose own values are finite and below 1e18 still matches the reference's
+    bytes, and Q4_0's NaN and Inf blocks too (a NaN is the block's absmax, as
+    torch's argmax takes it); the oracle returns bytes for every type."""
+    x, qw, ref = nonfinite_case()
+    assert {k.split(".")[0] for k in ref} == set(ORACLE_TYPES) - {"q3_k", "q6_k", "iq2_xxs"}
+    n_clean = 0
+    for key, expect in sorted(ref.items()):
+        qtype, mode = key.split(".")
+        clean = clean_blocks(x, TYPES[qtype][1])
+        got = oracle.quantize(qtype, x, qw if mode == "imat" else None, n_threads=4)
+        same = block_identical(got, expect, qtype)
+        assert same[clean].all(), f"{key}: {int((clean & ~same).sum())} finite blocks differ"
+        assert (~clean).any() and clean.any()
+        if qtype == "q4_0":
+            assert same.all(), f"q4_0: {int((~same).sum())} non-finite blocks differ"
+        n_clean += int(clean.sum())
+    for qtype in ("q3_k", "q6_k", "iq2_xxs"):
+        assert oracle.quantize(qtype, x, qw, n_threads=4).shape[0] == x.shape[0]
+    assert n_clean >= 300
 
 
 @pytest.mark.parametrize("qtype", ["q4_k", "iq2_s", "iq3_xxs"])
