@@ -48,6 +48,9 @@ QS_DEV float clampf(float v, float lo, float hi) { return fminf(fmaxf(v, lo), hi
 // here, so the compiler can neither recompute it later from its inputs (which
 // would keep those live instead) nor hoist work that uses it out of a loop.
 QS_DEV void keep_in_register(float& v) { asm volatile("" : "+v"(v)); }
+// pred holds on some active lane of the wave
+QS_DEV bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
+
 template <int N>
 QS_DEV void keep_in_registers(float (&v)[N]) {
 #pragma unroll

@@ -199,6 +199,7 @@ QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const fl
     float suml2 = cascade8_of<N>([&](int i) { return (w[i] * L[i]) * L[i]; });
 #pragma unroll 1
     for (int pass = 0; pass < 5; pass++) {
+        bool changed = false;
 #pragma unroll
         for (int i = 0; i < N; i++) {
             const float xi = x[i], Li = L[i];
@@ -216,8 +217,14 @@ QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const fl
                 L[i] = newl;
                 sumlx = slx2;
                 suml2 = sl22;
+                changed = true;
             }
         }
+        // a pass that commits nothing leaves L, sumlx and suml2 as they were,
+        // so every later pass repeats it (the C loop's early break, which the
+        // reference's five passes stand for, kq_common.py:121-136): the wave stops
+        // once none of its lanes committed
+        if (!wave_any(changed)) break;
     }
     float scale = suml2 > 0 ? sumlx / fmaxf(suml2, F32_TINY) : 0.0f;
     if (dead) {
@@ -307,6 +314,7 @@ QS_DEV float q3_fit(const float (&x)[N], int nmax, float (&L)[N]) {
     float sumlx = seq_sum(t), suml2 = seq_sum(u);
 #pragma unroll 1
     for (int pass = 0; pass < 5; pass++) {
+        bool changed = false;
 #pragma unroll
         for (int i = 0; i < N; i++) {
             const float xi = x[i], wi = w[i], Li = L[i];
@@ -320,8 +328,10 @@ QS_DEV float q3_fit(const float (&x)[N], int nmax, float (&L)[N]) {
                 L[i] = newl;
                 sumlx = slx2;
                 suml2 = sl22;
+                changed = true;
             }
         }
+        if (!wave_any(changed)) break;        // as in qp_fit (qx_common.py:100-114)
     }
     const float scale = suml2 > 0 ? sumlx / suml2 : 0.0f;
 #pragma unroll
