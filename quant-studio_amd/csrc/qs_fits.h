@@ -8,6 +8,7 @@
 #pragma once
 
 #include "qs_device.h"
+#include "qs_wave.h"
 
 namespace qs {
 
@@ -158,41 +159,29 @@ QS_DEV float qkx_level(const QkxResult& r, float x, float fmax) {
     return r.degen ? 0.0f : clampf(rintf(r.isc * (x - r.mn)), 0.0f, fmax);
 }
 
-// make_qp_quants_eager kq_common.py:99-141 for N sub-block scales (N = 8, 16).
-// Writes the levels to L and returns the scale.
-template <int N>
-QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const float (&steps)[8], float (&L)[N]) {
-    const float fmax = (float)nmax;
-    float mx = x[0];
-#pragma unroll
-    for (int i = 1; i < N; i++) mx = fmaxf(mx, x[i]);
-    const bool dead = mx < GROUP_MAX_EPS;
-    const float mxs = dead ? 1.0f : mx;
+// make_qp_quants_eager kq_common.py:99-141, in three parts: qp_trial (one
+// trial's weighted error), qp_finish (levels, sums and refinement passes for
+// the chosen iscale) and the choice between them, made by qp_fit on one lane
+// or by qp_fit_spread over several.
 
-    float iscale = rdiv(fmax, mxs);
-    float best_mse;
-    {
-        const float r = 1.0f / iscale;
-        best_mse = cascade8_of<N>([&](int i) {
-            float l0 = rintf(iscale * x[i]);
-            float d = x[i] - r * l0;
-            return w[i] * (d * d);
-        });
-    }
-#pragma unroll 1
-    for (int s = 0; s < 8; s++) {
-        const float isc = rdiv(steps[s], mxs);
-        const float r = 1.0f / isc;
-        const float mse = cascade8_of<N>([&](int i) {
-            float l = fminf(rintf(isc * x[i]), fmax);
-            float d = x[i] - r * l;
-            return w[i] * (d * d);
-        });
-        if (mse < best_mse) {
-            best_mse = mse;
-            iscale = isc;
-        }
-    }
+// The weighted error of the levels rint(isc * x), clamped to fmax unless
+// `clamp` is false: the first pass (kq_common.py:107-109) does not clamp.
+template <int N>
+QS_DEV float qp_trial(const float (&x)[N], const float (&w)[N], float isc, float fmax, bool clamp) {
+    const float r = 1.0f / isc;
+    return cascade8_of<N>([&](int i) {
+        float l = rintf(isc * x[i]);
+        l = clamp ? fminf(l, fmax) : l;
+        float d = x[i] - r * l;
+        return w[i] * (d * d);
+    });
+}
+
+// kq_common.py:118-141 for the chosen iscale: writes the levels to L and
+// returns the scale.
+template <int N>
+QS_DEV float qp_finish(const float (&x)[N], const float (&w)[N], float fmax, float iscale, bool dead,
+                       float (&L)[N]) {
 #pragma unroll
     for (int i = 0; i < N; i++) L[i] = fminf(rintf(iscale * x[i]), fmax);
     float sumlx = cascade8_of<N>([&](int i) { return (w[i] * x[i]) * L[i]; });
@@ -233,6 +222,79 @@ QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const fl
         for (int i = 0; i < N; i++) L[i] = 0.0f;
     }
     return scale;
+}
+
+
+template <int N>
+QS_DEV float qp_max(const float (&x)[N]) {
+    float mx = x[0];
+#pragma unroll
+    for (int i = 1; i < N; i++) mx = fmaxf(mx, x[i]);
+    return mx;
+}
+
+// make_qp_quants_eager on one lane (N = 8, 16, 32). Writes the levels to L
+// and returns the scale.
+template <int N>
+QS_DEV float qp_fit(const float (&x)[N], const float (&w)[N], int nmax, const float (&steps)[8], float (&L)[N]) {
+    const float fmax = (float)nmax;
+    const float mx = qp_max(x);
+    const bool dead = mx < GROUP_MAX_EPS;
+    const float mxs = dead ? 1.0f : mx;
+
+    float iscale = rdiv(fmax, mxs);
+    float best_mse = qp_trial<N>(x, w, iscale, fmax, false);
+#pragma unroll 1
+    for (int s = 0; s < 8; s++) {
+        const float isc = rdiv(steps[s], mxs);
+        const float mse = qp_trial<N>(x, w, isc, fmax, true);
+        if (mse < best_mse) {
+            best_mse = mse;
+            iscale = isc;
+        }
+    }
+    return qp_finish<N>(x, w, fmax, iscale, dead, L);
+}
+
+// make_qp_quants_eager for one superblock's N sub-block scales (or mins),
+// spread over P consecutive lanes (c = 0..P-1) that all hold x and w. The
+// nine trials (the first pass, then the eight candidates) do not depend on
+// each other, only the choice among them does, so lane c runs trials c,
+// c + P, ...; their (error, iscale) pairs meet in xch (18 floats of LDS) and
+// every lane makes the reference's choice in trial order (the first strict
+// minimum) and finishes the fit. Every lane of the wave must call it (it
+// holds a wave barrier); all P lanes return the same scale and levels.
+template <int N, int P, bool WL = false>
+QS_DEV float qp_fit_spread(const float (&x)[N], const float (&w)[N], int nmax, const float (&steps)[8],
+                           float (&L)[N], int c, float* xch) {
+    static_assert(P >= 1 && P <= 9, "one to nine lanes share the trials");
+    const float fmax = (float)nmax;
+    const float mx = qp_max(x);
+    const bool dead = mx < GROUP_MAX_EPS;
+    const float mxs = dead ? 1.0f : mx;
+#pragma unroll
+    for (int k = 0; k < (9 + P - 1) / P; k++) {
+        const int e = c + k * P;
+        if (e < 9) {
+            float num = fmax;        // trial 0: nmax / max; trial e: candidate e - 1
+#pragma unroll
+            for (int j = 0; j < 8; j++) num = e == j + 1 ? steps[j] : num;
+            const float isc = rdiv(num, mxs);
+            xch[2 * e] = qp_trial<N>(x, w, isc, fmax, e != 0);
+            xch[2 * e + 1] = isc;
+        }
+    }
+    wave_sync<WL>();
+    float best_mse = xch[0], iscale = xch[1];
+#pragma unroll
+    for (int e = 1; e < 9; e++) {
+        const float mse = xch[2 * e];
+        if (mse < best_mse) {
+            best_mse = mse;
+            iscale = xch[2 * e + 1];
+        }
+    }
+    return qp_finish<N>(x, w, fmax, iscale, dead, L);
 }
 
 // make_qx_quants_eager qx_common.py:52-82 for one group of 16 values.

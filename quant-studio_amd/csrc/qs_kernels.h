@@ -382,20 +382,26 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(IMAT ? 3 : 4
     int ls, lm;
     float d16, m16;
     if constexpr (IMAT) {
-        if (g < 2) {
+        // make_qp over the 8 scales (lanes 0-3 of the superblock) and the 8
+        // mins (lanes 4-7), each fit's trials spread over its four lanes;
+        // the exchange reuses the sigma2 scratch
+        const int f = g >> 2, c = g & 3;
+        {
             float xv[8], wv[8], L[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                xv[i] = g == 0 ? s.sc[slot][i] : s.mn[slot][i];
+                xv[i] = f == 0 ? s.sc[slot][i] : s.mn[slot][i];
                 wv[i] = s.sw[slot][i];
             }
-            const float sc = qp_fit<8>(xv, wv, 63, qps.v, L);
-            s.hdr[slot][g] = sc;
+            const float sc = qp_fit_spread<8, 4>(xv, wv, 63, qps.v, L, c, s.tmp[slot] + 18 * f);
+            if (c == 0) {
+                s.hdr[slot][f] = sc;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int li = (int)L[i] & 0xFF;
-                if (g == 0) s.ls[slot][i] = li;
-                else s.lm[slot][i] = li;
+                for (int i = 0; i < 8; i++) {
+                    const int li = (int)L[i] & 0xFF;
+                    if (f == 0) s.ls[slot][i] = li;
+                    else s.lm[slot][i] = li;
+                }
             }
         }
         wave_sync();
@@ -684,20 +690,25 @@ __global__ __launch_bounds__(64) void k_q2_k(KArgs a, Steps steps, QpSteps qps) 
         s.mn[slot][g] = r.the_min;
         s.sw[slot][g] = cascade8_sum(w);
         wave_sync();
-        if (g < 2) {
+        {
+            // the 16 scales on lanes 0-7 of the superblock, the 16 mins on
+            // lanes 8-15, each fit's trials spread over its eight lanes
+            const int f = g >> 3, c = g & 7;
             float xv[16], wv[16], L[16];
 #pragma unroll
             for (int i = 0; i < 16; i++) {
-                xv[i] = g == 0 ? s.sc[slot][i] : s.mn[slot][i];
+                xv[i] = f == 0 ? s.sc[slot][i] : s.mn[slot][i];
                 wv[i] = s.sw[slot][i];
             }
-            const float sc = qp_fit<16>(xv, wv, 15, qps.v, L);
-            s.hdr[slot][g] = sc;
+            const float sc = qp_fit_spread<16, 8>(xv, wv, 15, qps.v, L, c, s.tmp[slot] + 18 * f);
+            if (c == 0) {
+                s.hdr[slot][f] = sc;
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int li = (int)L[i] & 0xFF;
-                if (g == 0) s.ls[slot][i] = li;
-                else s.lm[slot][i] = li;
+                for (int i = 0; i < 16; i++) {
+                    const int li = (int)L[i] & 0xFF;
+                    if (f == 0) s.ls[slot][i] = li;
+                    else s.lm[slot][i] = li;
+                }
             }
         }
         wave_sync();
