@@ -304,6 +304,20 @@ struct QxResult {
     bool live;
 };
 
+// sums of one make_qx trial: the levels clamp(rint(isc * x), -nmax, nmax - 1)
+// and their seq-sums sum w x L, sum w L^2 (qx_common.py:61-63, :68-70)
+template <int N>
+QS_DEV float2 qx_trial(const float (&x)[N], const float (&w)[N], float isc, float fmax) {
+    float t[N], u[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        float La = clampf(rintf(isc * x[i]), -fmax, fmax - 1.0f);
+        t[i] = (w[i] * x[i]) * La;
+        u[i] = (w[i] * La) * La;
+    }
+    return make_float2(seq_sum(t), seq_sum(u));
+}
+
 template <int N>
 QS_DEV QxResult qx_fit(const float (&x)[N], const float (&w)[N], int nmax, const Steps& steps) {
     const float fmax = (float)nmax;
@@ -311,15 +325,9 @@ QS_DEV QxResult qx_fit(const float (&x)[N], const float (&w)[N], int nmax, const
     const float mx = absmax_first(x, amax);
     const bool live = amax >= GROUP_MAX_EPS;
     const float mxs = live ? mx : 1.0f;
-    float t[N], u[N];
     const float iscale = rdiv(-fmax, mxs);
-#pragma unroll
-    for (int i = 0; i < N; i++) {
-        float L = clampf(rintf(iscale * x[i]), -fmax, fmax - 1.0f);
-        t[i] = (w[i] * x[i]) * L;
-        u[i] = (w[i] * L) * L;
-    }
-    const float sumlx = seq_sum(t), suml2 = seq_sum(u);
+    const float2 s0 = qx_trial<N>(x, w, iscale, fmax);
+    const float sumlx = s0.x, suml2 = s0.y;
     float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx, best_isc = iscale;
     float step_next = steps.v[0];      // loaded one candidate ahead (Q3_K 4%, Q6_K 2% faster)
@@ -328,18 +336,64 @@ QS_DEV QxResult qx_fit(const float (&x)[N], const float (&w)[N], int nmax, const
         const float step = step_next;
         step_next = steps.v[s + 1 < 40 ? s + 1 : 39];
         const float isc = rdiv(-step, mxs);
-#pragma unroll
-        for (int i = 0; i < N; i++) {
-            float La = clampf(rintf(isc * x[i]), -fmax, fmax - 1.0f);
-            t[i] = (w[i] * x[i]) * La;
-            u[i] = (w[i] * La) * La;
-        }
-        const float slx = seq_sum(t), sl2 = seq_sum(u);
+        const float2 sc = qx_trial<N>(x, w, isc, fmax);
+        const float slx = sc.x, sl2 = sc.y;
         if (sl2 > 0 && slx * slx > best * sl2) {
             const float cand = slx / sl2;
             scale = cand;
             best = cand * slx;
             best_isc = isc;
+        }
+    }
+    QxResult r;
+    r.scale = live ? scale : 0.0f;
+    r.isc = best_isc;
+    r.live = live;
+    return r;
+}
+
+// make_qx_quants_eager for one superblock's N sub-block scales, spread over
+// P consecutive lanes (c = 0..P-1) that all hold x and w, for NS candidates
+// (the host's steps.n). A trial's levels and sums depend only on its iscale,
+// not on earlier accepts, so lane c forms the sums of trials c, c + P, ...
+// (trial 0: the first pass; trial e: candidate e - 1); they meet in xch
+// (3 (NS + 1) floats of LDS) and every lane runs the accept chain in
+// candidate order. Every lane of the wave must call it (it holds a wave
+// barrier); all P lanes return the same result.
+template <int N, int P, int NS, bool WL = false>
+QS_DEV QxResult qx_fit_spread(const float (&x)[N], const float (&w)[N], int nmax, const Steps& steps,
+                              int c, float* xch) {
+    const float fmax = (float)nmax;
+    float amax;
+    const float mx = absmax_first(x, amax);
+    const bool live = amax >= GROUP_MAX_EPS;
+    const float mxs = live ? mx : 1.0f;
+#pragma unroll
+    for (int k = 0; k < (NS + 1 + P - 1) / P; k++) {
+        const int e = c + k * P;
+        if (e <= NS) {
+            float num = fmax;
+#pragma unroll
+            for (int j = 0; j < NS; j++) num = e == j + 1 ? steps.v[j] : num;
+            const float isc = rdiv(-num, mxs);
+            const float2 sc = qx_trial<N>(x, w, isc, fmax);
+            xch[3 * e] = sc.x;
+            xch[3 * e + 1] = sc.y;
+            xch[3 * e + 2] = isc;
+        }
+    }
+    wave_sync<WL>();
+    const float sumlx = xch[0], suml2 = xch[1];
+    float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx, best_isc = xch[2];
+#pragma unroll 1
+    for (int e = 1; e <= NS; e++) {
+        const float slx = xch[3 * e], sl2 = xch[3 * e + 1];
+        if (sl2 > 0 && slx * slx > best * sl2) {
+            const float cand = slx / sl2;
+            scale = cand;
+            best = cand * slx;
+            best_isc = xch[3 * e + 2];
         }
     }
     QxResult r;

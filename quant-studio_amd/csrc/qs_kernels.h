@@ -583,17 +583,18 @@ __global__ __launch_bounds__(64) void k_q3_k(KArgs a, Steps steps4, Steps steps3
         s.sc[slot][g] = r.scale;
         s.sw[slot][g] = seq_sum(w);
         wave_sync();
-        if (g == 0) {
+        {
+            // make_qx over the 16 sub-block scales, its 19 trials spread over
+            // the superblock's 16 lanes; the exchange reuses the x^2 staging
             float sc16[16], sw16[16];
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 sc16[j] = s.sc[slot][j];
                 sw16[j] = s.sw[slot][j];
             }
-            const QxResult r2 = qx_fit<16>(sc16, sw16, 32, steps32);
-            s.hdr[slot][0] = r2.scale;
-#pragma unroll
-            for (int j = 0; j < 16; j++) s.ls[slot][j] = (int)qx_level(r2, sc16[j], 32.0f);
+            const QxResult r2 = qx_fit_spread<16, 16, 18>(sc16, sw16, 32, steps32, g, s.v[slot]);
+            if (g == 0) s.hdr[slot][0] = r2.scale;
+            s.ls[slot][g] = (int)qx_level(r2, s.sc[slot][g], 32.0f);
         }
         wave_sync();
         ls6 = s.ls[slot][g];
