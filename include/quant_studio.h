@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define QS_ABI_VERSION 3
+#define QS_ABI_VERSION 4
 
 #define QS_EINVAL (-22)
 #define QS_ENOTSUP (-95)
@@ -153,8 +153,10 @@ const char *qs_last_error(void);
  * pinned buffers, quantized on the device and written with pwrite() at the
  * tensor's offset in the output file. The caller keeps the GGUF header,
  * tensor order and offsets, the type plan and the chunk size (--mem).
- * All calls on one pipeline come from one thread. Host memory passed in must
- * stay valid, and fd open, until qs_pipeline_finish() returns.
+ * Calls on one pipeline must not overlap; they may come from different
+ * threads (the command line creates its pipeline on a thread of its own and
+ * drives it from the main thread). Host memory passed in must stay valid, and
+ * fd open, until qs_pipeline_finish() returns.
  */
 typedef struct qs_pipeline qs_pipeline;
 
@@ -180,6 +182,20 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline 
 int qs_pipeline_quantize(qs_pipeline *p, int ggml_type, int src_type, const void *src,
                          int64_t n_rows, int64_t k, const float *imatrix,
                          int64_t rows_per_chunk, int fd, int64_t out_offset);
+
+/* As qs_pipeline_quantize, with the rows read from the file src_fd (rows
+ * contiguous from byte src_offset) with pread() instead of copied from host
+ * memory. The command line passes its input GGUF this way: the copies read the
+ * page cache without mapping it, so they take no page faults and the process
+ * has no multi-GB mapping to tear down (unmapping 8 GB of faulted-in rows took
+ * 0.04-0.12 s on the MI355X machine's host). The same pipeline.quantize_tensor
+ * call of the reference (quant-studio.py:180-213, which reads the rows through
+ * gguf-py's memory map). src_fd must stay open until qs_pipeline_finish()
+ * returns; a read error or a file that ends inside the tensor fails the call
+ * with QS_EIO. */
+int qs_pipeline_quantize_fd(qs_pipeline *p, int ggml_type, int src_type, int src_fd,
+                            int64_t src_offset, int64_t n_rows, int64_t k, const float *imatrix,
+                            int64_t rows_per_chunk, int fd, int64_t out_offset);
 
 /* Queue a write of nbytes host bytes at out_offset of fd, in order with the
  * quantized chunks (a passthrough tensor, copy_tensor quant-studio.py:235-241). */

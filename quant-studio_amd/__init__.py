@@ -26,7 +26,7 @@ from .gguf_types import GGMLQuantizationType, LlamaFileType
 
 PKG = Path(__file__).resolve().parent
 LIB_PATH = PKG / "_build" / "libqs_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib: ctypes.CDLL | None = None
 
@@ -108,6 +108,10 @@ def library() -> ctypes.CDLL:
         L.qs_pipeline_quantize.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                            ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
                                            ctypes.c_int64, ctypes.c_int, ctypes.c_int64]
+        L.qs_pipeline_quantize_fd.restype = ctypes.c_int
+        L.qs_pipeline_quantize_fd.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                              ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                              ctypes.c_int64, ctypes.c_int, ctypes.c_int64]
         L.qs_pipeline_write.restype = ctypes.c_int
         L.qs_pipeline_write.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                         ctypes.c_int64]

@@ -349,7 +349,25 @@ def preallocate(fd: int, size: int) -> bool:
     return size > 0 and fn(fd, 0, 0, size) == 0
 
 
-def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: dict) -> None:
+def start_device(req: Request):
+    """Starts the native pipeline's creation on a thread of its own (a
+    PipelineStart) once the request is parsed, so the device's initialisation
+    overlaps loading the imatrix, parsing the input and planning the tensors;
+    None when the requested device is absent. Which device is used, and every
+    error, is still decided by write_output in the reference's order (its
+    pipeline is created after the plan, quant-studio.py:445-449)."""
+    from .pipeline import PipelineStart, device_count
+    try:
+        dev = int(req.device.split(":", 1)[1]) if ":" in req.device else 0
+    except ValueError:
+        return None
+    return PipelineStart(dev) if 0 <= dev < device_count() else None
+
+
+def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: dict,
+                 start=None) -> None:
+    """Streams the planned tensors through the native pipeline into req.dst;
+    `start` is start_device()'s pipeline in the making, if any."""
     from . import library, row_bytes, SQRT_ROUNDING
     from .pipeline import NativePipeline, PipelineError, Readahead, device_count
     dev = device_index(req, device_count())
@@ -381,7 +399,8 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
     t0 = time.time()
     ahead = Readahead([st.tensor for st in steps])
     try:
-        with NativePipeline(dev, fd) as pipe:
+        early = start.take(fd) if start is not None and start.device == dev else None
+        with early or NativePipeline(dev, fd) as pipe:
             for i, (st, info) in enumerate(zip(steps, writer.infos)):
                 t, off = st.tensor, base + info[3]
                 ahead.advance(t.nbytes)
@@ -391,7 +410,7 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
                     qw = imatrix.get(t.name) if st.spec.uses_imatrix else None
                     rows = max(1, req.mem_bytes // (t.ne[0] * st.spec.bytes_per_elem))
                     nbytes = pipe.quantize_tensor(t, int(st.dst), qw, rows, off,
-                                                  row_bytes(int(st.dst), t.ne[0]))
+                                                  row_bytes(int(st.dst), t.ne[0]), reader.fileno())
                 total_in += t.nbytes
                 total_out += nbytes
                 shape = "x".join(str(d) for d in t.ne)
@@ -415,16 +434,21 @@ def main(argv: list[str] | None = None) -> int:
     device_shown = "rocm" if req.device not in ("cpu", "mps") else f"{req.device} (on rocm)"
     print(f"quant-studio: {req.src} -> {req.dst} [{req.option.name}] device={device_shown} "
           f"mem={req.mem_text} sqrt-rounding={req.sqrt_rounding}")
-    imatrix: dict[str, np.ndarray] = {}
-    if req.imatrix is not None:
-        imatrix = load_imatrix(req.imatrix)
-        print(f"imatrix: {len(imatrix)} entries from {req.imatrix}")
-    reader = GGUFReader(req.src)
-    if "general.architecture" not in reader.values():
-        sys.exit("error: input has no general.architecture key")
-    steps = plan_tensors(req, reader, imatrix)
-    if req.dry_run:
-        print_plan(steps)
-        return 0
-    write_output(req, reader, steps, imatrix)
+    start = None if req.dry_run else start_device(req)
+    try:
+        imatrix: dict[str, np.ndarray] = {}
+        if req.imatrix is not None:
+            imatrix = load_imatrix(req.imatrix)
+            print(f"imatrix: {len(imatrix)} entries from {req.imatrix}")
+        reader = GGUFReader(req.src)
+        if "general.architecture" not in reader.values():
+            sys.exit("error: input has no general.architecture key")
+        steps = plan_tensors(req, reader, imatrix)
+        if req.dry_run:
+            print_plan(steps)
+            return 0
+        write_output(req, reader, steps, imatrix, start)
+    finally:
+        if start is not None:
+            start.close()           # a pipeline that was not taken (an error stopped the run)
     return 0

@@ -1,5 +1,6 @@
-// Host pipeline of the command line: mapped GGUF rows -> pinned staging ->
-// HBM -> quantizer -> pinned -> pwrite at the tensor's file offset.
+// Host pipeline of the command line: GGUF rows (pread from the input file, or
+// copied from host memory) -> pinned staging -> HBM -> quantizer -> pinned ->
+// pwrite at the tensor's file offset.
 //
 // Replaces the reference's CudaPipeline (quant-studio.py:148-213),
 // OutputWriter (:103-131) and copy_tensor (:235-241):
@@ -8,8 +9,8 @@
 //     copy of chunk i+2, the H2D of chunk i+1, the kernel of chunk i and the
 //     D2H and file write of earlier chunks overlap, and a writer a few chunks
 //     behind does not hold back the next uploads;
-//   - the mapping -> pinned copy of a chunk split over a pool of threads (one
-//     thread caps the pipeline well below the PCIe rate);
+//   - the read (or copy) into pinned memory of a chunk split over a pool of
+//     threads (one thread caps the pipeline well below the PCIe rate);
 //   - H2D and D2H on two copy streams (so the next chunk's upload never queues
 //     behind this chunk's download, which waits for its kernel), kernels on
 //     two compute streams taken in turn, all ordered by per-slot events; the
@@ -24,6 +25,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <condition_variable>
 #include <cstring>
@@ -42,7 +44,7 @@ using qs_host::fail;
 
 namespace {
 
-constexpr size_t kCopyPart = size_t(4) << 20;     // smallest share of a chunk copy per thread
+constexpr size_t kCopyPart = size_t(1) << 20;     // smallest share of a chunk copy per thread
 
 // Fixed pool running the parts of one chunk copy; run() returns when all are done.
 class CopyPool {
@@ -270,6 +272,38 @@ struct qs_pipeline {
     }
 };
 
+// Where a tensor's rows come from: host memory (normally the input file's
+// mapping) or a file read with pread(), which copies from the page cache
+// without mapping the pages into the process (no page faults in the copies,
+// no page-table teardown when the mapping goes).
+struct RowSource {
+    const char* mem = nullptr;
+    int fd = -1;
+    int64_t off = 0;
+};
+
+// One share of a chunk's staging copy; returns 0 or an errno value.
+static int copy_rows(const RowSource& src, size_t from, char* to, size_t n) {
+    if (!src.mem) {
+        while (n) {
+            const ssize_t r = pread(src.fd, to, std::min(n, size_t(1) << 30), (off_t)(src.off + (int64_t)from));
+            if (r < 0 && errno == EINTR) continue;
+            if (r < 0) return errno;
+            if (r == 0) return EIO;       // the file ends inside the tensor
+            to += r;
+            from += (size_t)r;
+            n -= (size_t)r;
+        }
+        return 0;
+    }
+    std::memcpy(to, src.mem + from, n);
+    return 0;
+}
+
+static int pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const RowSource& rows,
+                             int64_t n_rows, int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
+                             int64_t out_offset);
+
 extern "C" {
 
 int qs_device_count(void) {
@@ -324,6 +358,28 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
                          int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
                          int64_t out_offset) {
     qs_host::clear_error();
+    RowSource rows;
+    rows.mem = static_cast<const char*>(src);
+    return pipeline_quantize(p, ggml_type, src_type, rows, n_rows, k, imatrix, rows_per_chunk, fd, out_offset);
+}
+
+int qs_pipeline_quantize_fd(qs_pipeline* p, int ggml_type, int src_type, int src_fd, int64_t src_offset,
+                            int64_t n_rows, int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
+                            int64_t out_offset) {
+    qs_host::clear_error();
+    if (src_fd < 0 || src_offset < 0)
+        return fail(QS_EINVAL, "bad input fd %d / offset %lld", src_fd, (long long)src_offset);
+    RowSource rows;
+    rows.fd = src_fd;
+    rows.off = src_offset;
+    return pipeline_quantize(p, ggml_type, src_type, rows, n_rows, k, imatrix, rows_per_chunk, fd, out_offset);
+}
+
+}  // extern "C"
+
+static int pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const RowSource& src,
+                             int64_t n_rows, int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
+                             int64_t out_offset) {
     if (!p) return fail(QS_EINVAL, "null pipeline");
     if (int rc = p->check_writer()) return rc;
     const int esz = elem_size(src_type);
@@ -341,14 +397,13 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
         return fail(QS_EINVAL, "%lld x %lld values exceed the 2^34 per tensor", (long long)n_rows,
                     (long long)k);
     if (n_rows == 0) return 0;
-    if (!src) return fail(QS_EINVAL, "null src");
+    if (!src.mem && src.fd < 0) return fail(QS_EINVAL, "null src");
     if (qs_host::quantizer_requires_imatrix(ggml_type) && !imatrix)
         return fail(QS_EINVAL, "ggml type %d requires an imatrix", ggml_type);
     const bool use_qw = imatrix && qs_type_uses_imatrix(ggml_type) == 1;
     hipError_t e = hipSetDevice(p->device);
     if (e != hipSuccess) return p->hip_fail(e, "hipSetDevice");
     const int64_t in_row = k * esz;
-    const char* rows = static_cast<const char*>(src);
 
     for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_chunk) {
         const int64_t n = std::min(rows_per_chunk, n_rows - r0);
@@ -377,16 +432,23 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
             return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)n,
                         (long long)in_row);
         }
-        // mapping -> pinned, in parts of at least kCopyPart bytes
-        const char* from = rows + r0 * in_row;
+        // rows -> pinned, in parts of at least kCopyPart bytes
+        const size_t from = (size_t)(r0 * in_row);
         char* to = static_cast<char*>(si.in_pin.p);
         const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), nin / kCopyPart));
         std::vector<std::function<void()>> tasks;
+        std::atomic<int> read_err{0};
         for (size_t i = 0; i < parts; i++) {
             const size_t a = nin * i / parts, b = nin * (i + 1) / parts;
-            tasks.emplace_back([=] { std::memcpy(to + a, from + a, b - a); });
+            tasks.emplace_back([&src, &read_err, from, to, a, b] {
+                if (const int e = copy_rows(src, from + a, to + a, b - a)) read_err.store(e);
+            });
         }
         p->pool->run(tasks);
+        if (const int re = read_err.load()) {
+            if (p->err.empty()) p->err = std::string("reading the input rows failed: ") + std::strerror(re);
+            return fail(QS_EIO, "%s", p->err.c_str());
+        }
         if (nqw) std::memcpy(si.qw_pin.p, imatrix, nqw);
 
         // the upload overwrites x_dev / qw_dev once the kernel that read them is done
@@ -417,6 +479,8 @@ int qs_pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const void
     }
     return 0;
 }
+
+extern "C" {
 
 int qs_pipeline_write(qs_pipeline* p, const void* src, int64_t nbytes, int fd, int64_t out_offset) {
     qs_host::clear_error();

@@ -82,6 +82,7 @@ class TensorInfo:
     offset: int                    # relative to the data section
     nbytes: int
     data: np.ndarray | None = None  # uint8 view into the mapped file
+    file_offset: int = -1          # absolute offset of the data in the file (-1: not from a file)
 
     @property
     def n_elements(self) -> int:
@@ -149,7 +150,7 @@ class GGUFReader:
             start = self.data_offset + off
             if start + nbytes > len(self._mm):
                 raise ValueError(f"{path}: tensor {name} extends past the end of the file")
-            self.tensors.append(TensorInfo(name, ne, gtype, off, nbytes, base[start:start + nbytes]))
+            self.tensors.append(TensorInfo(name, ne, gtype, off, nbytes, base[start:start + nbytes], start))
 
     def _u32(self, buf) -> int:
         v = struct.unpack_from("<I", buf, self._pos)[0]
@@ -174,6 +175,10 @@ class GGUFReader:
         v = struct.unpack_from(fmt, buf, self._pos)[0]
         self._pos += struct.calcsize(fmt)
         return v
+
+    def fileno(self) -> int:
+        """Descriptor of the input file (the pipeline reads tensor rows with pread)."""
+        return self._f.fileno()
 
     def get(self, name: str, default=None):
         kv = self.kv.get(name)

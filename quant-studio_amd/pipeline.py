@@ -96,14 +96,36 @@ def device_count() -> int:
     return int(library().qs_device_count())
 
 
+# Input bytes per staged chunk. --mem bounds a chunk (the reference's budget
+# per row chunk, quant-studio.py:457); the pipeline stages at most this much
+# per chunk within it. The output does not depend on the chunking, and with
+# chunks of this size the mapping copy, H2D, kernel, D2H and write of
+# consecutive chunks overlap inside every tensor instead of across whole
+# tensors, and the pinned slots stay small. Measured on the synthetic
+# 4B-class model, warm (process wall, one MI355X): IQ2_XXS 0.77 s with whole
+# tensors per chunk (--mem 4G) -> 0.61 s at 16 MiB (8 MiB 0.62, 32 MiB 0.62,
+# 64 MiB 0.67, 128 MiB 0.73); Q4_K_M 0.74 -> 0.49 s; IQ3_XXS 0.74 -> 0.60 s
+# (at 32 MiB); IQ2_S 0.89 -> 0.76 s (at 32 MiB).
+STAGE_BYTES = 16 << 20
+
+
+def default_copy_threads() -> int:
+    return min(16, len(os.sched_getaffinity(0)))
+
+
 class NativePipeline:
-    def __init__(self, device: int, fd: int, slots: int = 3, copy_threads: int | None = None):
+    def __init__(self, device: int, fd: int, slots: int = 3, copy_threads: int | None = None,
+                 handle: ctypes.c_void_p | None = None):
+        """A pipeline on `device` writing to fd, or the one `handle` holds
+        (made by PipelineStart)."""
         self.L = library()
         self.fd = fd
-        n = copy_threads or min(16, len(os.sched_getaffinity(0)))
-        h = ctypes.c_void_p()
-        self._check(self.L.qs_pipeline_create(int(device), int(slots), int(n), ctypes.byref(h)))
-        self.h = h
+        if handle is None:
+            handle = ctypes.c_void_p()
+            self._check(self.L.qs_pipeline_create(int(device), int(slots),
+                                                  int(copy_threads or default_copy_threads()),
+                                                  ctypes.byref(handle)))
+        self.h = handle
         self._keep: list = []          # host buffers that must outlive finish()
 
     @staticmethod
@@ -112,20 +134,29 @@ class NativePipeline:
             raise PipelineError(last_error())
 
     def quantize_tensor(self, t: TensorInfo, ggml_type: int, qw: np.ndarray | None,
-                        rows_per_chunk: int, offset: int, row_bytes: int) -> int:
-        """Queue tensor t (rows from the input mapping) for quantization to
-        ggml_type, written at `offset` of the output file; returns its bytes."""
+                        rows_per_chunk: int, offset: int, row_bytes: int, src_fd: int = -1) -> int:
+        """Queue tensor t for quantization to ggml_type, written at `offset` of
+        the output file, staged in chunks of at most rows_per_chunk rows and
+        STAGE_BYTES input bytes; returns its bytes. With src_fd (the input
+        file's descriptor, t read from it) the rows are read with pread at
+        t.file_offset, else copied from t's mapping."""
         rows = t.rows()
         n_rows = rows.shape[0]
         k = t.ne[0]
+        rows_per_chunk = max(1, min(int(rows_per_chunk), STAGE_BYTES // max(1, rows.shape[1])))
         qptr = None
         if qw is not None:
             qw = np.ascontiguousarray(qw[:k], dtype=np.float32)
             self._keep.append(qw)
             qptr = qw.ctypes.data
-        self._check(self.L.qs_pipeline_quantize(self.h, int(ggml_type), SRC_IDS[t.ggml_type],
-                                                rows.ctypes.data, n_rows, k, qptr, int(rows_per_chunk),
-                                                self.fd, int(offset)))
+        if src_fd >= 0 and t.file_offset >= 0:
+            self._check(self.L.qs_pipeline_quantize_fd(self.h, int(ggml_type), SRC_IDS[t.ggml_type],
+                                                       int(src_fd), int(t.file_offset), n_rows, k, qptr,
+                                                       int(rows_per_chunk), self.fd, int(offset)))
+        else:
+            self._check(self.L.qs_pipeline_quantize(self.h, int(ggml_type), SRC_IDS[t.ggml_type],
+                                                    rows.ctypes.data, n_rows, k, qptr, int(rows_per_chunk),
+                                                    self.fd, int(offset)))
         return n_rows * row_bytes
 
     def write(self, data: np.ndarray, offset: int) -> int:
@@ -150,3 +181,41 @@ class NativePipeline:
 
     def __exit__(self, *exc):
         self.close()
+
+
+class PipelineStart:
+    """qs_pipeline_create on a thread of its own. The thread makes just that C
+    call, which releases the GIL, so the device's initialisation (its first
+    stream creation sets up the device's queues: ~0.08 s on the MI355X) runs
+    while the calling thread goes on with Python work. take() joins it and
+    returns the NativePipeline, or None if the creation failed (the caller
+    then creates one itself and sees the error on its own thread)."""
+
+    def __init__(self, device: int, slots: int = 3, copy_threads: int | None = None):
+        import threading
+        self.device = int(device)
+        self._L = library()
+        self._h = ctypes.c_void_p()
+        self._rc: int | None = None
+        create = self._L.qs_pipeline_create
+        args = (self.device, int(slots), int(copy_threads or default_copy_threads()), ctypes.byref(self._h))
+
+        def run() -> None:
+            self._rc = create(*args)
+
+        self._thread = threading.Thread(target=run, name="qs-pipeline-create", daemon=True)
+        self._thread.start()
+
+    def take(self, fd: int) -> NativePipeline | None:
+        self._thread.join()
+        if self._rc != 0 or not self._h.value:
+            return None
+        h, self._h = self._h, ctypes.c_void_p()
+        return NativePipeline(self.device, fd, handle=h)
+
+    def close(self) -> None:
+        """Release a pipeline that was not taken."""
+        self._thread.join()
+        if self._rc == 0 and self._h.value:
+            self._L.qs_pipeline_destroy(self._h)
+            self._h = ctypes.c_void_p()

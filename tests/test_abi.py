@@ -27,7 +27,8 @@ def test_header_declares_the_api():
     names = set(declared_functions())
     assert {"qs_abi_version", "qs_row_bytes", "qs_quantize", "qs_last_error",
             "qs_type_supported", "qs_type_needs_imatrix", "qs_type_uses_imatrix",
-            "qs_device_count", "qs_pipeline_create", "qs_pipeline_quantize", "qs_pipeline_write",
+            "qs_device_count", "qs_pipeline_create", "qs_pipeline_quantize", "qs_pipeline_quantize_fd",
+            "qs_pipeline_write",
             "qs_pipeline_finish", "qs_pipeline_destroy", "qs_init", "qs_set_sqrt_rounding",
             "qs_get_sqrt_rounding"} <= names
 
@@ -36,7 +37,7 @@ def test_library_exports_every_declared_symbol(qs):
     L = qs.library()
     for name in declared_functions():
         assert hasattr(L, name), f"libqs_hip.so does not export {name}"
-    assert L.qs_abi_version() == qs.ABI_VERSION == 3
+    assert L.qs_abi_version() == qs.ABI_VERSION == 4
 
 
 @pytest.mark.parametrize("qtype", sorted(TYPES))
@@ -162,6 +163,7 @@ def test_pipeline_rejects_bad_arguments_without_device_work(qs):
     assert "not present" in qs.last_error() and not h.value
     assert L.qs_pipeline_create(0, 3, 4, None) == -22
     assert L.qs_pipeline_quantize(None, 12, 30, None, 1, 256, None, 1, 1, 0) == -22
+    assert L.qs_pipeline_quantize_fd(None, 12, 30, 0, 0, 1, 256, None, 1, 1, 0) == -22
     assert L.qs_pipeline_write(None, None, 0, 1, 0) == -22
     assert L.qs_pipeline_finish(None) == -22
     L.qs_pipeline_destroy(None)

@@ -185,6 +185,58 @@ def test_pipeline_chunks_match_single_call_and_report_write_errors(tmp_path):
         os.close(fd)
 
 
+def test_pipeline_reads_rows_from_the_file(tmp_path):
+    """qs_pipeline_quantize_fd (rows read with pread at a file offset) writes
+    the oracle's bytes for any chunking, bf16 and f32 rows at unaligned file
+    offsets alike; a tensor that runs past the end of the file fails with
+    QS_EIO naming the read, and an invalid descriptor or offset is refused."""
+    import ctypes
+    import os
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    rng = np.random.default_rng(9)
+    x = (rng.normal(size=(29, 512)) * 0.02).astype(np.float32)
+    qw = rng.lognormal(size=512).astype(np.float32)
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)          # bf16 by truncation
+    xbf = (xb.astype(np.uint32) << 16).view(np.float32)
+    src = tmp_path / "rows.bin"
+    lead = 37                                                    # an odd file offset
+    src.write_bytes(bytes(lead) + x.tobytes() + xb.tobytes())
+    cases = [(GT.F32, x, x, lead), (GT.BF16, xb, xbf, lead + x.nbytes)]
+    sfd = os.open(src, os.O_RDONLY)
+    try:
+        for gt, raw, xf, off in cases:
+            ref = oracle.quantize("q4_k", xf, qw)
+            info = io.TensorInfo("t", (512, 29), gt, 0, raw.nbytes, raw.view(np.uint8).reshape(-1), off)
+            for rows_per_chunk in (1, 6, 29):
+                path = tmp_path / f"o{int(gt)}_{rows_per_chunk}.bin"
+                fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+                try:
+                    with pl.NativePipeline(0, fd) as p:
+                        p.quantize_tensor(info, int(GT.Q4_K), qw, rows_per_chunk, 0,
+                                          qs.row_bytes(int(GT.Q4_K), 512), sfd)
+                        p.finish()
+                finally:
+                    os.close(fd)
+                got = np.frombuffer(path.read_bytes(), np.uint8).reshape(ref.shape)
+                assert np.array_equal(got, ref), (gt.name, rows_per_chunk)
+        fd = os.open(tmp_path / "short.bin", os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+        try:
+            with pl.NativePipeline(0, fd) as p:
+                # 4 more rows than the file holds after the bf16 block
+                rc = p.L.qs_pipeline_quantize_fd(p.h, int(GT.Q4_K), 30, sfd, lead + x.nbytes, 33, 512,
+                                                 None, 64, fd, 0)
+                assert rc == -5 and "reading the input rows failed" in qs.last_error()
+                assert p.L.qs_pipeline_quantize_fd(p.h, int(GT.Q4_K), 30, -1, 0, 1, 512, None, 1,
+                                                   fd, 0) == -22
+                assert p.L.qs_pipeline_quantize_fd(p.h, int(GT.Q4_K), 30, sfd, -1, 1, 512, None, 1,
+                                                   fd, 0) == -22
+        finally:
+            os.close(fd)
+    finally:
+        os.close(sfd)
+
+
 @pytest.mark.parametrize("scheme,ftype", [("Q4_K_M", 15), ("Q5_K_S", 16), ("IQ4_XS", 30)])
 def test_shape_fallback_types_end_to_end(tmp_path, scheme, ftype):
     """288-value rows fall back to Q5_0 / Q5_1 / Q8_0 / IQ4_NL (scheme.py:364-384)."""
