@@ -187,7 +187,8 @@ def copy_kernel_rate(torch, dev, traffic: int, steps: int = 24) -> float:
                                ctypes.c_void_p(stream.cuda_stream))
         if rc:
             raise RuntimeError(f"qs_calib_copy failed ({rc})")
-    _, ms = time_steps(torch, [launch], steps, 5)
+    # median of five short regions, as the 32-value rows it is compared with
+    _, ms = sorted(time_steps(torch, [launch], steps, 5) for _ in range(5))[2]
     del bufs
     torch.cuda.empty_cache()
     return 2 * n / (ms * 1e-3)
@@ -703,8 +704,12 @@ def main() -> int:
     for qtype in sel:
         for imat in modes_of(qtype):
             key = f"{qtype}{'+imat' if imat else ''}"
-            st, km = time_steps(torch, shape_launches(qs, qtype, imat, xs_rot, qws, outs_for(qtype)),
-                                max(10, args.steps // 4), 20)
+            # the 32-value launches take ~13 us, so one late launch moves a
+            # 10-step region by several percent: median of five regions
+            runs = [time_steps(torch, shape_launches(qs, qtype, imat, xs_rot, qws, outs_for(qtype)),
+                               max(10, args.steps // 4), 20)
+                    for _ in range(5 if qtype in B32_TYPES else 1)]
+            st, km = sorted(runs)[len(runs) // 2]
             a = sum(algorithmic_bytes(qtype, r * k, k) for r, k in SHAPES) / (st * 1e-3) / 1e9
             n_insts = valu_counts.get(key)
             print(f"bench: {key}: {km:.4f} ms per launch", file=sys.stderr, flush=True)
