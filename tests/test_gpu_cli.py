@@ -237,6 +237,35 @@ def test_pipeline_reads_rows_from_the_file(tmp_path):
         os.close(sfd)
 
 
+def test_pipeline_made_on_another_thread(tmp_path):
+    """PipelineStart: a pipeline created on its own thread works when taken on
+    this one (the oracle's bytes), can be taken only once, and one that is
+    never taken is released by close()."""
+    import os
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    rng = np.random.default_rng(10)
+    x = (rng.normal(size=(9, 512)) * 0.02).astype(np.float32)
+    info = io.TensorInfo("t", (512, 9), GT.F32, 0, x.nbytes, x.view(np.uint8).reshape(-1))
+    ref = oracle.quantize("q6_k", x, None)
+    path = tmp_path / "o.bin"
+    fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        start = pl.PipelineStart(0)
+        p = start.take(fd)
+        assert p is not None and start.take(fd) is None
+        with p:
+            p.quantize_tensor(info, int(GT.Q6_K), None, 4, 0, qs.row_bytes(int(GT.Q6_K), 512))
+            p.finish()
+        start.close()
+    finally:
+        os.close(fd)
+    assert np.array_equal(np.frombuffer(path.read_bytes(), np.uint8).reshape(ref.shape), ref)
+    unused = pl.PipelineStart(0)
+    unused.close()
+    unused.close()
+
+
 @pytest.mark.parametrize("scheme,ftype", [("Q4_K_M", 15), ("Q5_K_S", 16), ("IQ4_XS", 30)])
 def test_shape_fallback_types_end_to_end(tmp_path, scheme, ftype):
     """288-value rows fall back to Q5_0 / Q5_1 / Q8_0 / IQ4_NL (scheme.py:364-384)."""
