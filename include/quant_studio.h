@@ -148,10 +148,10 @@ const char *qs_last_error(void);
 /* ---- host pipeline of the command line ----
  *
  * Replaces the reference's CudaPipeline (quant-studio.py:148-213), its
- * OutputWriter (:103-131) and copy_tensor (:235-241): rows are read from host
- * memory (normally the input file's mapping) chunk by chunk, staged through
- * pinned buffers, quantized on the device and written with pwrite() at the
- * tensor's offset in the output file. The caller keeps the GGUF header,
+ * OutputWriter (:103-131) and copy_tensor (:235-241): rows are read chunk by
+ * chunk from the input file (pread, qs_pipeline_quantize_fd) or from host
+ * memory (qs_pipeline_quantize) into pinned buffers, quantized on the device
+ * and written with pwrite() at the tensor's offset in the output file. The caller keeps the GGUF header,
  * tensor order and offsets, the type plan and the chunk size (--mem).
  * Calls on one pipeline must not overlap; they may come from different
  * threads (the command line creates its pipeline on a thread of its own and
@@ -169,7 +169,7 @@ int qs_device_count(void);
  * copy, H2D and kernel of consecutive chunks overlapped), max(8, 2 n_slots)
  * output slots (device output and its pinned copy, so a writer a few chunks
  * behind does not hold back the next uploads), and n_copy_threads host
- * threads (1..64) for the mapping -> pinned copies. */
+ * threads (1..64) that read or copy each chunk's rows into pinned memory. */
 int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline **out);
 
 /* Queue one tensor: n_rows rows of k values of src_type at host address src

@@ -1,9 +1,10 @@
 """Host pipeline of the command line, driven from Python over the C ABI.
 
 The staging itself is native (qs_pipeline_* in libqs_hip.so): a ring of
-pinned slots, a thread pool for the mapping -> pinned copies, H2D/D2H on a
-copy stream, kernels on a compute stream, and a writer thread that pwrite()s
-each chunk at its own file offset once its D2H event has fired. It replaces
+pinned slots, a thread pool that reads each chunk's rows from the input file
+(pread) into its slot, H2D and D2H on copy streams, kernels on two compute
+streams, and a writer thread that pwrite()s each chunk at its own file offset
+once its D2H event has fired. It replaces
 the reference's CudaPipeline, OutputWriter and copy_tensor
 (quant-studio.py:103-131, :148-213, :235-241). Python keeps what the
 reference keeps in Python: the GGUF header, tensor order and offsets, the type
@@ -36,10 +37,12 @@ class Readahead:
     the pipeline's copies (madvise MADV_WILLNEED, in plan order, from a
     thread of its own, a window at a time), at most `budget` bytes past the
     tensor being queued.
-    The copies fault the mapping in a few MB at a time and the pipeline waits
-    for a free slot between chunks, so with a cold page cache the disk idles
-    between reads; with the requests queued ahead it streams. Best effort:
-    a failing madvise is ignored (the copies fault the pages in anyway)."""
+    The pipeline reads a chunk at a time and waits for a free slot between
+    chunks, so with a cold page cache the disk would idle between reads; with
+    the requests queued ahead it streams. The advice goes through the file's
+    mapping but maps nothing into the process (no page-table entries are
+    made). Best effort: a failing madvise is ignored (the reads fetch the
+    pages anyway)."""
 
     MADV_WILLNEED = 3
 
@@ -99,7 +102,7 @@ def device_count() -> int:
 # Input bytes per staged chunk. --mem bounds a chunk (the reference's budget
 # per row chunk, quant-studio.py:457); the pipeline stages at most this much
 # per chunk within it. The output does not depend on the chunking, and with
-# chunks of this size the mapping copy, H2D, kernel, D2H and write of
+# chunks of this size the read, H2D, kernel, D2H and write of
 # consecutive chunks overlap inside every tensor instead of across whole
 # tensors, and the pinned slots stay small. Measured on the synthetic
 # 4B-class model, warm (process wall, one MI355X): IQ2_XXS 0.77 s with whole
