@@ -24,9 +24,20 @@ namespace qs {
 // each list starts on a CH-entry boundary of nbr and is padded to a multiple
 // of CH, so a lane fetches a chunk of CH candidates with one vector load
 // (CH = 8 for the IQ2 grids, 4 for the IQ3 grids, whose lists are short).
+//
+// cinfo_red has the same layout and points at each list's reduced copy: the
+// list without the entries that change a proper superset of an earlier
+// entry's changed values (against the code's levels) and agree with it on
+// those. A search may read it when the code's level is the best level of
+// every value for its distance terms (iq_codes<..., PRUNE>): every left-out
+// entry then has each term >= that earlier entry's, so a distance >= it and
+// can never be the first minimum; the reduced list keeps the list's order, so
+// its first minimum is the list's. (Grids built without reduced lists point
+// cinfo_red at the full entries.)
 struct IqTabDev {
     const uint16_t* grid;     // grid codes (BITS-bit levels per value)
     const uint32_t* cinfo;    // code -> packed kmap / list position / length
+    const uint32_t* cinfo_red;  // code -> the reduced list's position / length
     const uint16_t* nbr;      // neighbour grid indices, (distance, index) order
     int code0;                // grid index of the all-zero code (0 if off-grid)
 };
@@ -132,24 +143,51 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // nothing (their result is unused).
 //   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
 //   res:  LDS, 64 keys
-template <int BITS, int NV, int NSUB, int N>
-QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB]) {
+//
+// PRUNE: the search of subgroup s (weights wv, scale sc: the very operands
+// of its distance terms) reads the code's reduced list when the code's level
+// is the best of the grid's levels in each of its values. A term is
+// t(v) = (w*d)*d with d = sc*v - x; for sc > 0 and w >= 0 it is monotone in
+// |d| and d rises with v, so it falls while d < 0 and rises after: the code's
+// level is the best when its term is 0 (no term is negative) or strictly
+// below both neighbouring levels' (the grid's levels are 0..3 for IQ2 and
+// 0..7 for IQ3; a strictly smaller neighbour on the rising side rules out a
+// falling side beyond it). A NaN term, a tie or sc <= 0 reads the full list.
+template <int BITS, int NV, int NSUB, bool PRUNE = false, int N>
+QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB],
+                     const float (&wv)[N], float sc) {
     // all subgroups' codes first, so their cinfo loads are in flight together
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
+    constexpr float GMAX = BITS == 2 ? 3.0f : 7.0f;     // the grid's largest level
     int code[NSUB];
+    bool best[NSUB];
 #pragma unroll
     for (int s = 0; s < NSUB; s++) {
         code[s] = 0;
+        best[s] = PRUNE && sc > 0.0f;
 #pragma unroll
         for (int j = 0; j < NV; j++) {
-            float t = inv * xv[NV * s + j];
+            const float x = xv[NV * s + j];
+            float t = inv * x;
             t = t - 1.0f;
             t = 0.5f * t;
-            code[s] |= (int)clampf(rintf(t), 0.0f, LMAX) << (BITS * j);
+            const float lf = clampf(rintf(t), 0.0f, LMAX);
+            code[s] |= (int)lf << (BITS * j);
+            if constexpr (PRUNE) {
+                const float v = 2.0f * lf + 1.0f, w = wv[NV * s + j];
+                auto term = [&](float lv) {
+                    float d = sc * lv;
+                    d = d - x;
+                    return (w * d) * d;
+                };
+                const float tu = term(v), tm = term(v - 2.0f), tp = term(v + 2.0f);
+                const bool ok = tu == 0.0f || ((lf == 0.0f || tu < tm) && (lf == GMAX || tu < tp));
+                best[s] = best[s] && ok;
+            }
         }
     }
 #pragma unroll
-    for (int s = 0; s < NSUB; s++) ci[s] = T.cinfo[code[s]];
+    for (int s = 0; s < NSUB; s++) ci[s] = best[s] ? T.cinfo_red[code[s]] : T.cinfo[code[s]];
 }
 
 // First minimum of one chunk (CH list slots from slot CH*kc) as a 64-bit key
@@ -469,7 +507,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gi[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4>(T, xval, inv, ci);
+        iq_codes<2, 8, 4, true>(T, xval, inv, ci, waux, sc);
         static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
@@ -489,7 +527,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gp[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4>(T, xval, inv, ci);
+        iq_codes<2, 8, 4, true>(T, xval, inv, ci, waux, scale);
         static_for<0, 4>([&](auto S) {
             gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
@@ -591,7 +629,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         int gi[2];
         bool on[2];
         uint32_t ci[2];
-        iq_codes<2, 8, 2>(T, xval, inv, ci);
+        iq_codes<2, 8, 2, !IS_S>(T, xval, inv, ci, waux, sc);
         gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
         gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
         float sumqx, sumq2;
@@ -613,7 +651,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
         uint32_t ci[2];
-        iq_codes<2, 8, 2>(T, xval, inv, ci);
+        iq_codes<2, 8, 2, !IS_S>(T, xval, inv, ci, waux, scale);
         const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
                                                           need && !og[0], on);
         const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
@@ -756,7 +794,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int gi[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL>(T, xval, inv, ci);
+        iq_codes<3, 4, NSL, true>(T, xval, inv, ci, waux, sc);
         static_for<0, NSL>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
@@ -784,7 +822,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int w2[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL>(T, xval, inv2, ci);
+        iq_codes<3, 4, NSL, true>(T, xval, inv2, ci, waux, scale);
         static_for<0, NSL>([&](auto S) {
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);
