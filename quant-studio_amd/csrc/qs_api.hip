@@ -136,6 +136,7 @@ struct HostTab {
     std::vector<uint16_t> grid, nbr;
     std::vector<uint32_t> cinfo;       // IQ2 layout described at qs::IqTabDev
     std::vector<uint32_t> cinfo_red;   // the same for the reduced lists (qs::IqTabDev)
+    std::vector<uint32_t> cinfo_red2;  // and for the lists reduced for a clamped level (qs::IqTabDev)
     int code0 = 0;
     bool ok = true;
 };
@@ -148,14 +149,18 @@ struct HostTab {
 // appended in code order and the ranges joined in order, so the tables are
 // the sequential build's byte for byte.
 //
-// With `reduce`, every list also gets a reduced copy (cinfo_red, stored after
+// With reduce >= 1, every list also gets a reduced copy (cinfo_red, stored after
 // all full lists): an entry is left out when an earlier entry of the list
 // changes a proper subset of the values it changes (against the code's
 // levels) and agrees with it on those. When the code's level is the best
 // level of every value for the search's distance terms, the left-out entry
 // has every term >= the earlier entry's, so it can never be the list's first
-// minimum (qs::iq_codes decides which list a search reads).
-HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch, int maxch, bool reduce) {
+// minimum (qs::iq_codes decides which list a search reads). With reduce 2, a
+// second reduced copy (cinfo_red2, after the first) leaves an entry out only
+// when that earlier entry also makes every raise from the code's clamped top
+// level (IQ2: level 2) to the grid's level 3 that it makes: it stays valid
+// where such a value's level-3 term is below its level-2 term.
+HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch, int maxch, int reduce) {
     const int nsub = bits == 2 ? 8 : 4, lmask = (1 << bits) - 1, lmax = bits == 2 ? 2 : 7;
     const int ksize = bits == 2 ? 43692 : 4096;
     HostTab t;
@@ -172,10 +177,12 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
         for (int j = 0; j < nsub; j++) gl[i * nsub + j] = 2 * ((grid[i] >> (bits * j)) & lmask) + 1;
     // lists of codes [c0, c1): cinfo entries with starts relative to the range
     struct Part {
-        std::vector<uint16_t> nbr, red;
+        std::vector<uint16_t> nbr, red, red2;
         bool ok = true;
     };
     t.cinfo_red.assign(ksize, 0);
+    t.cinfo_red2.assign(ksize, 0);
+    const int vclamp = 2 * lmax + 1, vtop = 2 * lmask + 1;     // values of the code's and the grid's top levels
     auto build_range = [&](int c0, int c1, Part& part) {
         std::vector<int> d2(gs);
         for (int c = c0; c < c1; c++) {
@@ -208,7 +215,7 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
                 for (int i = 0; i < gs; i++)
                     if (d2[i] == small[r]) part.nbr.push_back((uint16_t)i);
             const size_t len = part.nbr.size() - start;
-            if (reduce) {
+            if (reduce > 0) {
                 // changed values of each entry (bit j: its level differs from the code's)
                 std::vector<uint32_t> chg(len);
                 for (size_t k = 0; k < len; k++) {
@@ -218,23 +225,37 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
                         if (gl[gi * nsub + j] != p[j]) m |= 1u << j;
                     chg[k] = m;
                 }
-                const size_t rstart = part.red.size();
+                // values where an entry raises the code's clamped top level to the grid's top
+                std::vector<uint32_t> up(len);
+                for (size_t k = 0; k < len && reduce == 2; k++) {
+                    const int gi = part.nbr[start + k];
+                    uint32_t m = 0;
+                    for (int j = 0; j < nsub; j++)
+                        if (vclamp != vtop && p[j] == vclamp && gl[gi * nsub + j] == vtop) m |= 1u << j;
+                    up[k] = m;
+                }
+                const size_t rstart = part.red.size(), rstart2 = part.red2.size();
                 for (size_t jj = 0; jj < len; jj++) {
                     const int gj = part.nbr[start + jj];
-                    bool drop = false;
-                    for (size_t ii = 0; ii < jj && !drop; ii++) {
+                    bool drop = false, drop2 = false;
+                    for (size_t ii = 0; ii < jj && !(reduce == 2 ? drop2 : drop); ii++) {
                         if ((chg[ii] & ~chg[jj]) || chg[ii] == chg[jj]) continue;   // not a proper subset
                         const int gi = part.nbr[start + ii];
                         bool agree = true;
                         for (int j = 0; j < nsub; j++)
                             if ((chg[ii] >> j) & 1u) agree = agree && gl[gi * nsub + j] == gl[gj * nsub + j];
-                        drop = agree;
+                        if (!agree) continue;
+                        drop = true;
+                        drop2 = !(up[jj] & ~chg[ii]);
                     }
                     if (!drop) part.red.push_back((uint16_t)gj);
+                    if (!drop2 && reduce == 2) part.red2.push_back((uint16_t)gj);
                 }
-                const size_t rlen = part.red.size() - rstart;
+                const size_t rlen = part.red.size() - rstart, rlen2 = part.red2.size() - rstart2;
                 part.red.resize((part.red.size() + ch - 1) / ch * ch, 0);
+                part.red2.resize((part.red2.size() + ch - 1) / ch * ch, 0);
                 t.cinfo_red[c] = (uint32_t)((rstart / ch) << 12) | (uint32_t)rlen;
+                t.cinfo_red2[c] = (uint32_t)((rstart2 / ch) << 12) | (uint32_t)rlen2;
             }
             part.nbr.resize((part.nbr.size() + ch - 1) / ch * ch, 0);
             t.cinfo[c] = (uint32_t)((start / ch) << 12) | (uint32_t)len;
@@ -258,9 +279,12 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
     for (auto& th : threads) th.join();
     // join the ranges in code order, moving each range's starts by the lists
     // before it; the reduced lists follow all full lists
-    size_t base = 0, total = 0;
-    for (int k = 0; k < nthr; k++) total += parts[k].nbr.size();
-    size_t rbase = total;
+    size_t base = 0, total = 0, total_red = 0;
+    for (int k = 0; k < nthr; k++) {
+        total += parts[k].nbr.size();
+        total_red += parts[k].red.size();
+    }
+    size_t rbase = total, rbase2 = total + total_red;
     for (int k = 0; k < nthr; k++) {
         const int c0 = (int)((int64_t)ksize * k / nthr), c1 = (int)((int64_t)ksize * (k + 1) / nthr);
         for (int c = c0; c < c1; c++) {
@@ -268,22 +292,32 @@ HostTab build_host_tab(const uint16_t* grid, int gs, int bits, int nwant, int ch
             const size_t start = ((t.cinfo[c] >> 12) & 0x7ffffu) + base / ch;
             t.ok = t.ok && start < (1u << 19);
             t.cinfo[c] = (uint32_t)(start << 12) | (t.cinfo[c] & 0xfffu);
-            if (reduce) {
+            if (reduce > 0) {
                 const size_t rstart = ((t.cinfo_red[c] >> 12) & 0x7ffffu) + rbase / ch;
                 t.ok = t.ok && rstart < (1u << 19) && (t.cinfo_red[c] & 0xfffu) > 0;
                 t.cinfo_red[c] = (uint32_t)(rstart << 12) | (t.cinfo_red[c] & 0xfffu);
+            }
+            if (reduce == 2) {
+                const size_t rstart2 = ((t.cinfo_red2[c] >> 12) & 0x7ffffu) + rbase2 / ch;
+                t.ok = t.ok && rstart2 < (1u << 19) && (t.cinfo_red2[c] & 0xfffu) > 0;
+                t.cinfo_red2[c] = (uint32_t)(rstart2 << 12) | (t.cinfo_red2[c] & 0xfffu);
             }
         }
         t.nbr.insert(t.nbr.end(), parts[k].nbr.begin(), parts[k].nbr.end());
         base += parts[k].nbr.size();
         rbase += parts[k].red.size();
+        rbase2 += parts[k].red2.size();
         t.ok = t.ok && parts[k].ok;
     }
     for (int k = 0; k < nthr; k++) t.nbr.insert(t.nbr.end(), parts[k].red.begin(), parts[k].red.end());
+    for (int k = 0; k < nthr; k++) t.nbr.insert(t.nbr.end(), parts[k].red2.begin(), parts[k].red2.end());
     // on-grid codes, codes without a list and tables without reduced lists
-    // read the full entry
-    for (int c = 0; c < ksize; c++)
-        if (!reduce || kmap[c] >= 0 || !(t.cinfo[c] & 0xfffu)) t.cinfo_red[c] = t.cinfo[c];
+    // read the full entry; tables without the second reduced copy read the
+    // first in its place
+    for (int c = 0; c < ksize; c++) {
+        if (reduce == 0 || kmap[c] >= 0 || !(t.cinfo[c] & 0xfffu)) t.cinfo_red[c] = t.cinfo[c];
+        if (reduce < 2 || kmap[c] >= 0 || !(t.cinfo[c] & 0xfffu)) t.cinfo_red2[c] = t.cinfo_red[c];
+    }
     return t;
 }
 
@@ -294,12 +328,15 @@ const HostTab& host_tab(int id) {
     std::call_once(once[id], [id] {
         switch (id) {
         // IQ2_S's lists (one distance) have no entry whose changes contain
-        // another's, so its grid keeps only the full lists
-        case IQT_G2_256: tabs[id] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_CH, qs::IQ2_256_MAXCH, true); break;
-        case IQT_G2_512: tabs[id] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_CH, qs::IQ2_512_MAXCH, true); break;
-        case IQT_G2_1024: tabs[id] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_CH, qs::IQ2_1024_MAXCH, false); break;
-        case IQT_G3_256: tabs[id] = build_host_tab(QS_GRID3_256, 256, 3, 2, qs::IQ3_CH, qs::IQ3_256_MAXCH, true); break;
-        default: tabs[id] = build_host_tab(QS_GRID3_512, 512, 3, 3, qs::IQ3_CH, qs::IQ3_512_MAXCH, true); break;
+        // another's, so its grid keeps only the full lists; the second
+        // reduced copy is read by the IQ2_XXS search only (qs::iq_codes
+        // PRUNE 2: on IQ2_XS its bookkeeping cost more than it saved, and
+        // the IQ3 grids' top level is the code's)
+        case IQT_G2_256: tabs[id] = build_host_tab(QS_GRID2_256, 256, 2, 2, qs::IQ2_CH, qs::IQ2_256_MAXCH, 2); break;
+        case IQT_G2_512: tabs[id] = build_host_tab(QS_GRID2_512, 512, 2, 2, qs::IQ2_CH, qs::IQ2_512_MAXCH, 1); break;
+        case IQT_G2_1024: tabs[id] = build_host_tab(QS_GRID2_1024, 1024, 2, 1, qs::IQ2_CH, qs::IQ2_1024_MAXCH, 0); break;
+        case IQT_G3_256: tabs[id] = build_host_tab(QS_GRID3_256, 256, 3, 2, qs::IQ3_CH, qs::IQ3_256_MAXCH, 1); break;
+        default: tabs[id] = build_host_tab(QS_GRID3_512, 512, 3, 3, qs::IQ3_CH, qs::IQ3_512_MAXCH, 1); break;
         }
     });
     return tabs[id];
@@ -407,14 +444,17 @@ bool device_tables_locked(int dev, int iq_table, const std::array<bool, SQM_N>& 
         const HostTab& h = host_tab(iq_table);
         qs::IqTabDev g{};
         g.grid = upload(h.grid);
-        g.cinfo = upload(h.cinfo);
-        g.cinfo_red = upload(h.cinfo_red);
+        // the three code tables back to back (qs::IqTabDev::cinfo)
+        std::vector<uint32_t> ci(h.cinfo);
+        ci.insert(ci.end(), h.cinfo_red.begin(), h.cinfo_red.end());
+        ci.insert(ci.end(), h.cinfo_red2.begin(), h.cinfo_red2.end());
+        g.cinfo = upload(ci);
+        g.ncodes = (int)h.cinfo.size();
         g.nbr = upload(h.nbr);
         g.code0 = h.code0;
-        if (!h.ok || !g.grid || !g.cinfo || !g.cinfo_red || !g.nbr) {
+        if (!h.ok || !g.grid || !g.cinfo || !g.nbr) {
             // nothing is kept from a failed upload; the next call tries again
-            for (const void* q : {(const void*)g.grid, (const void*)g.cinfo, (const void*)g.cinfo_red,
-                                  (const void*)g.nbr})
+            for (const void* q : {(const void*)g.grid, (const void*)g.cinfo, (const void*)g.nbr})
                 if (q) (void)hipFree(const_cast<void*>(q));
             return false;
         }

@@ -32,12 +32,22 @@ namespace qs {
 // every value for its distance terms (iq_codes<..., PRUNE>): every left-out
 // entry then has each term >= that earlier entry's, so a distance >= it and
 // can never be the first minimum; the reduced list keeps the list's order, so
-// its first minimum is the list's. (Grids built without reduced lists point
-// cinfo_red at the full entries.)
+// its first minimum is the list's. cinfo_red2 points at a second reduced
+// copy, which leaves an entry out only when the earlier entry also makes
+// every raise from the code's clamped top level (IQ2: level 2) to the grid's
+// level 3 that the left-out entry makes: it stays valid where the code's
+// level is every value's best level except at values on level 2 whose
+// level-3 term is lower (there level 2 still beats levels 0 and 1, so only a
+// raise to 3 lowers the term). Grids built without the second copy point
+// cinfo_red2 at the reduced lists, grids without reduced lists point both at
+// the full lists.
 struct IqTabDev {
     const uint16_t* grid;     // grid codes (BITS-bit levels per value)
-    const uint32_t* cinfo;    // code -> packed kmap / list position / length
-    const uint32_t* cinfo_red;  // code -> the reduced list's position / length
+    // code -> packed kmap / list position / length: the full lists' entries,
+    // then (at +ncodes) the reduced lists', then (at +2 ncodes) the
+    // clamp-tolerant reduced lists' (cinfo_red, cinfo_red2 above)
+    const uint32_t* cinfo;
+    int ncodes;
     const uint16_t* nbr;      // neighbour grid indices, (distance, index) order
     int code0;                // grid index of the all-zero code (0 if off-grid)
 };
@@ -152,19 +162,29 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // level is the best when its term is 0 (no term is negative) or strictly
 // below both neighbouring levels' (the grid's levels are 0..3 for IQ2 and
 // 0..7 for IQ3; a strictly smaller neighbour on the rising side rules out a
-// falling side beyond it). A NaN term, a tie or sc <= 0 reads the full list.
-template <int BITS, int NV, int NSUB, bool PRUNE = false, int N>
+// falling side beyond it). With PRUNE 2, where that fails only in values at
+// the clamped top level 2 (IQ2) whose level-3 term is below the level-2
+// term, the clamp-tolerant reduced list is read. A NaN term, a tie or
+// sc <= 0 reads the full list. PRUNE 0 reads the full lists.
+template <int BITS, int NV, int NSUB, int PRUNE = 0, int N>
 QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB],
                      const float (&wv)[N], float sc) {
     // all subgroups' codes first, so their cinfo loads are in flight together
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
     constexpr float GMAX = BITS == 2 ? 3.0f : 7.0f;     // the grid's largest level
-    int code[NSUB];
+    // per subgroup, PRUNE 1: whether the code's level is every value's best
+    // level, a bool (a lane mask: its updates take no VALU instructions);
+    // PRUNE 2: an int with bit 0 set when a value's code level is not its
+    // best level and bit 1 when the clamp-tolerant list does not hold either
+    // (two bools per subgroup spill in the IQ2_XXS search)
+    int code[NSUB], miss[NSUB];
     bool best[NSUB];
+    const bool prune = PRUNE > 0 && sc > 0.0f;
 #pragma unroll
     for (int s = 0; s < NSUB; s++) {
         code[s] = 0;
-        best[s] = PRUNE && sc > 0.0f;
+        best[s] = prune;
+        miss[s] = prune ? 0 : 3;
 #pragma unroll
         for (int j = 0; j < NV; j++) {
             const float x = xv[NV * s + j];
@@ -173,7 +193,7 @@ QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_
             t = 0.5f * t;
             const float lf = clampf(rintf(t), 0.0f, LMAX);
             code[s] |= (int)lf << (BITS * j);
-            if constexpr (PRUNE) {
+            if constexpr (PRUNE > 0) {
                 const float v = 2.0f * lf + 1.0f, w = wv[NV * s + j];
                 auto term = [&](float lv) {
                     float d = sc * lv;
@@ -182,12 +202,22 @@ QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_
                 };
                 const float tu = term(v), tm = term(v - 2.0f), tp = term(v + 2.0f);
                 const bool ok = tu == 0.0f || ((lf == 0.0f || tu < tm) && (lf == GMAX || tu < tp));
-                best[s] = best[s] && ok;
+                if constexpr (PRUNE == 2) {
+                    // the clamped top level with the grid's level 3 strictly better
+                    const bool up = LMAX < GMAX && lf == LMAX && tp < tu;
+                    miss[s] |= ok ? 0 : up ? 1 : 3;
+                } else {
+                    best[s] = best[s] && ok;
+                }
             }
         }
     }
 #pragma unroll
-    for (int s = 0; s < NSUB; s++) ci[s] = best[s] ? T.cinfo_red[code[s]] : T.cinfo[code[s]];
+    for (int s = 0; s < NSUB; s++) {
+        int tab = best[s] ? 1 : 0;
+        if constexpr (PRUNE == 2) tab = miss[s] == 0 ? 1 : miss[s] == 1 ? 2 : 0;
+        ci[s] = T.cinfo[code[s] + tab * T.ncodes];
+    }
 }
 
 // First minimum of one chunk (CH list slots from slot CH*kc) as a 64-bit key
@@ -507,7 +537,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gi[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4, true>(T, xval, inv, ci, waux, sc);
+        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, waux, sc);
         static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
@@ -527,7 +557,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gp[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4, true>(T, xval, inv, ci, waux, scale);
+        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, waux, scale);
         static_for<0, 4>([&](auto S) {
             gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
@@ -629,7 +659,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         int gi[2];
         bool on[2];
         uint32_t ci[2];
-        iq_codes<2, 8, 2, !IS_S>(T, xval, inv, ci, waux, sc);
+        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, waux, sc);
         gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
         gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
         float sumqx, sumq2;
@@ -651,7 +681,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
         uint32_t ci[2];
-        iq_codes<2, 8, 2, !IS_S>(T, xval, inv, ci, waux, scale);
+        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, waux, scale);
         const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
                                                           need && !og[0], on);
         const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
@@ -794,7 +824,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int gi[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL, true>(T, xval, inv, ci, waux, sc);
+        iq_codes<3, 4, NSL, 1>(T, xval, inv, ci, waux, sc);
         static_for<0, NSL>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
@@ -822,7 +852,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int w2[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL, true>(T, xval, inv2, ci, waux, scale);
+        iq_codes<3, 4, NSL, 1>(T, xval, inv2, ci, waux, scale);
         static_for<0, NSL>([&](auto S) {
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);

@@ -238,6 +238,38 @@ def test_empty_and_single_row(qs, dev):
     assert np.array_equal(got, oracle.quantize("q4_k", x, qw))
 
 
+def lattice_rows(rows: int, k: int, seed: int):
+    """Rows whose values are small integer multiples of a power of two (a
+    power of two per row, random signs, ~1 block in 8 of equal magnitudes)
+    with a power-of-two imatrix holding ~10% zeros: the IQ searches' level
+    terms then tie exactly, are exactly zero, and put values on the code's
+    clamped top level with the grid's top level better -- the cases in which
+    the searches choose between the full and the reduced neighbour lists."""
+    rng = np.random.default_rng(seed)
+    m = np.minimum(rng.geometric(0.25, (rows, k)) - 1, 15).astype(np.float64)
+    m *= rng.choice([-1.0, 1.0], (rows, k))
+    flat = rng.random((rows, k // 256)) < 0.125
+    m = np.where(np.repeat(flat, 256, axis=1), np.sign(m) * 3 + (m == 0), m)
+    a = m * 2.0 ** -rng.integers(5, 10, (rows, 1)).astype(np.float64)
+    qw = (2.0 ** rng.integers(-2, 3, k)) * (rng.random(k) >= 0.1)
+    return bf16_bits(a), qw.astype(np.float32)
+
+
+@pytest.mark.parametrize("qtype", ["iq2_xxs", "iq2_xs", "iq2_s", "iq3_xxs", "iq3_s"])
+def test_iq_searches_on_lattice_inputs(qs, dev, qtype):
+    """Lattice rows (exact ties, zero terms, clamped top levels) against the
+    oracle, with the imatrix and, where the type runs without one, without."""
+    x, qw = lattice_rows(384, 2560, seed=sum(map(ord, qtype)))
+    for q in (qw, None):
+        if q is None and qtype in NEEDS_IMATRIX:
+            continue
+        print(f"{qtype} imat={q is not None} lattice 384x2560", flush=True)
+        got = hip_quantize(qs, qtype, x, q, dev)
+        ref = oracle.quantize(qtype, x, q, n_threads=NTHREADS)
+        same = block_identical(got, ref, qtype)
+        assert same.all(), f"{qtype} imat={q is not None}: {int((~same).sum())}/{same.size} blocks differ"
+
+
 def test_iq2_xxs_full_ffn_down_tensor_heavy_tailed(qs, dev):
     """IQ2_XXS at full size: one 2560x9728 ffn_down tensor of
     Student-t (df 5) weights scaled to std 0.02 with a log-normal imatrix.
