@@ -174,11 +174,15 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline 
 
 /* Queue one tensor: n_rows rows of k values of src_type at host address src
  * (rows contiguous), quantized to ggml_type in chunks of rows_per_chunk rows
- * with the host imatrix (k floats or NULL; as qs_quantize), the output rows
- * written contiguously at out_offset of fd. Returns once every chunk is
- * queued; blocks only while all slots are busy. At most 2^34 values per
- * tensor (QS_EINVAL otherwise). One pipeline.quantize_tensor call of the
- * reference (quant-studio.py:180-213, driven from :453-461). */
+ * with the host imatrix (k floats or NULL; as qs_quantize; copied before the
+ * call returns), the output rows written contiguously at out_offset of fd.
+ * The rows of each chunk are read by the pipeline's threads while the
+ * previous chunk's upload, kernel and download are queued; the call returns
+ * with its last chunk still being read (that chunk is queued by the next call
+ * on the pipeline or by qs_pipeline_finish), and blocks only while all slots
+ * are busy. At most 2^34 values per tensor (QS_EINVAL otherwise). One
+ * pipeline.quantize_tensor call of the reference (quant-studio.py:180-213,
+ * driven from :453-461). */
 int qs_pipeline_quantize(qs_pipeline *p, int ggml_type, int src_type, const void *src,
                          int64_t n_rows, int64_t k, const float *imatrix,
                          int64_t rows_per_chunk, int fd, int64_t out_offset);
@@ -191,8 +195,8 @@ int qs_pipeline_quantize(qs_pipeline *p, int ggml_type, int src_type, const void
  * 0.04-0.12 s on the MI355X machine's host). The same pipeline.quantize_tensor
  * call of the reference (quant-studio.py:180-213, which reads the rows through
  * gguf-py's memory map). src_fd must stay open until qs_pipeline_finish()
- * returns; a read error or a file that ends inside the tensor fails the call
- * with QS_EIO. */
+ * returns; a read error or a file that ends inside the tensor fails this call,
+ * the next one or qs_pipeline_finish with QS_EIO. */
 int qs_pipeline_quantize_fd(qs_pipeline *p, int ggml_type, int src_type, int src_fd,
                             int64_t src_offset, int64_t n_rows, int64_t k, const float *imatrix,
                             int64_t rows_per_chunk, int fd, int64_t out_offset);
@@ -201,12 +205,13 @@ int qs_pipeline_quantize_fd(qs_pipeline *p, int ggml_type, int src_type, int src
  * quantized chunks (a passthrough tensor, copy_tensor quant-studio.py:235-241). */
 int qs_pipeline_write(qs_pipeline *p, const void *src, int64_t nbytes, int fd, int64_t out_offset);
 
-/* Wait until everything queued is written (OutputWriter.flush,
- * quant-studio.py:128-130); returns the first failure of any queued step. */
+/* Queue the last pending chunk and wait until everything queued is written
+ * (OutputWriter.flush, quant-studio.py:128-130); returns the first failure of
+ * any queued step. */
 int qs_pipeline_finish(qs_pipeline *p);
 
-/* Wait for queued work, then release the pipeline's threads, buffers,
- * streams and events. NULL is ignored. */
+/* Queue the last pending chunk and wait for queued work, then release the
+ * pipeline's threads, buffers, streams and events. NULL is ignored. */
 void qs_pipeline_destroy(qs_pipeline *p);
 
 #ifdef __cplusplus

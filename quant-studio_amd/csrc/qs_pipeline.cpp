@@ -10,7 +10,12 @@
 //     D2H and file write of earlier chunks overlap, and a writer a few chunks
 //     behind does not hold back the next uploads;
 //   - the read (or copy) into pinned memory of a chunk split over a pool of
-//     threads (one thread caps the pipeline well below the PCIe rate);
+//     threads (one thread caps the pipeline well below the PCIe rate), and
+//     run one chunk ahead of the launches: a queue call starts the pool on
+//     its chunk, then queues the previous chunk's upload, kernel and download
+//     while the pool reads, and leaves its own last chunk pending for the
+//     next call or qs_pipeline_finish, so reads overlap the launches and the
+//     caller's work between tensors;
 //   - H2D and D2H on two copy streams (so the next chunk's upload never queues
 //     behind this chunk's download, which waits for its kernel), kernels on
 //     two compute streams taken in turn, all ordered by per-slot events; the
@@ -62,15 +67,16 @@ public:
     }
     int size() const { return (int)threads_.size(); }
 
-    void run(std::vector<std::function<void()>>& tasks) {
-        if (tasks.size() == 1 || threads_.empty()) {
-            for (auto& t : tasks) t();
-            return;
-        }
-        std::unique_lock<std::mutex> l(m_);
+    // Start the tasks on the pool and return; wait() returns once every
+    // submitted task has run.
+    void submit(std::vector<std::function<void()>>& tasks) {
+        std::lock_guard<std::mutex> l(m_);
         for (auto& t : tasks) q_.push_back(std::move(t));
         pending_ += tasks.size();
         cv_.notify_all();
+    }
+    void wait() {
+        std::unique_lock<std::mutex> l(m_);
         done_cv_.wait(l, [this] { return pending_ == 0; });
     }
 
@@ -182,6 +188,16 @@ private:
     std::thread th_;
 };
 
+// Buffer sizes are rounded up (2 MiB for rows and outputs, 64 KiB for an
+// imatrix), so chunks whose byte counts differ by a few rows' worth (16 MiB
+// of input holds a whole number of rows of each width) and imatrices of
+// different widths reuse a slot's buffers: growing a device buffer frees the
+// old one, and hipFree waits for all work on the device.
+inline size_t alloc_size(size_t want) {
+    const size_t g = want > (size_t(64) << 10) ? size_t(2) << 20 : size_t(64) << 10;
+    return (std::max<size_t>(want, 1) + g - 1) / g * g;
+}
+
 struct PinnedBuf {
     void* p = nullptr;
     size_t n = 0;
@@ -190,7 +206,8 @@ struct PinnedBuf {
         if (p) (void)hipHostFree(p);
         p = nullptr;
         n = 0;
-        if (hipHostMalloc(&p, std::max<size_t>(want, 1), hipHostMallocDefault) != hipSuccess) return false;
+        want = alloc_size(want);
+        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return false;
         n = want;
         return true;
     }
@@ -209,7 +226,8 @@ struct DevBuf {
         if (p) (void)hipFree(p);
         p = nullptr;
         n = 0;
-        if (hipMalloc(&p, std::max<size_t>(want, 1)) != hipSuccess) return false;
+        want = alloc_size(want);
+        if (hipMalloc(&p, want) != hipSuccess) return false;
         n = want;
         return true;
     }
@@ -251,6 +269,18 @@ int elem_size(int src_type) {
 
 }  // namespace
 
+// A chunk whose rows are being read into its input slot and whose upload,
+// kernel and download are not queued yet.
+struct Chunk {
+    bool valid = false;
+    size_t slot = 0;          // input slot
+    int ggml_type = 0, src_type = 0;
+    int64_t n = 0, k = 0, in_row = 0;
+    size_t nin = 0, nout = 0, nqw = 0;
+    int fd = -1;
+    int64_t out_off = 0;
+};
+
 struct qs_pipeline {
     int device = 0;
     hipStream_t h2d = nullptr, d2h = nullptr, compute[2] = {nullptr, nullptr};
@@ -261,6 +291,8 @@ struct qs_pipeline {
     std::unique_ptr<CopyPool> pool;
     std::unique_ptr<Writer> writer;
     std::string err;          // first failure; every later call reports it
+    Chunk pending;            // read in flight on the pool, launch not queued
+    std::atomic<int> read_err{0};   // errno of a failed read (0: none)
 
     int check_writer() {
         if (err.empty()) err = writer->error();
@@ -377,6 +409,77 @@ int qs_pipeline_quantize_fd(qs_pipeline* p, int ggml_type, int src_type, int src
 
 }  // extern "C"
 
+// Wait for the pool's reads (the pending chunk's) and report a failed one.
+static int wait_reads(qs_pipeline* p) {
+    p->pool->wait();
+    if (const int re = p->read_err.exchange(0)) {
+        p->pending.valid = false;
+        if (p->err.empty()) p->err = std::string("reading the input rows failed: ") + std::strerror(re);
+        return fail(QS_EIO, "%s", p->err.c_str());
+    }
+    return 0;
+}
+
+// Queue the pending chunk (its rows are in its input slot): upload, kernel on
+// the next compute stream, download into an output slot, write job.
+static int launch_pending(qs_pipeline* p) {
+    if (!p->pending.valid) return 0;
+    const Chunk c = p->pending;
+    p->pending.valid = false;
+    InSlot& si = p->in_slots[c.slot];
+    OutSlot& so = p->out_slots[p->next_out];
+    p->next_out = (p->next_out + 1) % p->out_slots.size();
+    hipError_t e;
+    if (so.used) {
+        // out_pin: its write is done; out_dev: if it must grow, its D2H is done
+        p->writer->wait(so.write_seq);
+        if (int rc = p->check_writer()) return rc;
+        if (so.out_dev.n < c.nout && (e = hipEventSynchronize(so.d2h)) != hipSuccess)
+            return p->hip_fail(e, "D2H");
+    }
+    if (!so.out_pin.grow(c.nout) || !so.out_dev.grow(c.nout)) {
+        if (p->err.empty()) p->err = "out of memory staging a chunk";
+        return fail(QS_EIO, "out of memory staging the output of a chunk of %lld rows", (long long)c.n);
+    }
+    // the upload overwrites x_dev / qw_dev once the kernel that read them is done
+    if (si.used && (e = hipStreamWaitEvent(p->h2d, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+    if ((e = hipMemcpyAsync(si.x_dev.p, si.in_pin.p, c.nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
+        return p->hip_fail(e, "H2D");
+    if (c.nqw && (e = hipMemcpyAsync(si.qw_dev.p, si.qw_pin.p, c.nqw, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
+        return p->hip_fail(e, "H2D");
+    if ((e = hipEventRecord(si.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
+    si.used = true;
+    // the kernel writes out_dev once the D2H that read it is done
+    hipStream_t cs = p->compute[p->launches++ & 1];
+    if ((e = hipStreamWaitEvent(cs, si.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+    if (so.used && (e = hipStreamWaitEvent(cs, so.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+    const int rc = qs_quantize(c.ggml_type, c.src_type, si.x_dev.p, c.n, c.k, c.in_row,
+                               c.nqw ? static_cast<const float*>(si.qw_dev.p) : nullptr, so.out_dev.p,
+                               (int64_t)c.nout, cs);
+    if (rc) {
+        if (p->err.empty()) p->err = "quantizer launch failed";
+        return rc;
+    }
+    if ((e = hipEventRecord(si.kern, cs)) != hipSuccess) return p->hip_fail(e, "event");
+    if ((e = hipStreamWaitEvent(p->d2h, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
+    if ((e = hipMemcpyAsync(so.out_pin.p, so.out_dev.p, c.nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
+        return p->hip_fail(e, "D2H");
+    if ((e = hipEventRecord(so.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
+    so.used = true;
+    so.write_seq = p->writer->push({so.d2h, so.out_pin.p, c.nout, c.fd, c.out_off});
+    return 0;
+}
+
+// Queue what is still pending and wait for the reads.
+static int flush_pending(qs_pipeline* p) {
+    if (int rc = wait_reads(p)) return rc;
+    if (!p->err.empty()) {
+        p->pending.valid = false;
+        return fail(QS_EIO, "%s", p->err.c_str());
+    }
+    return launch_pending(p);
+}
+
 static int pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const RowSource& src,
                              int64_t n_rows, int64_t k, const float* imatrix, int64_t rows_per_chunk, int fd,
                              int64_t out_offset) {
@@ -406,76 +509,54 @@ static int pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const 
     const int64_t in_row = k * esz;
 
     for (int64_t r0 = 0; r0 < n_rows; r0 += rows_per_chunk) {
-        const int64_t n = std::min(rows_per_chunk, n_rows - r0);
-        const size_t nin = (size_t)(n * in_row), nout = (size_t)(n * out_row), nqw = use_qw ? (size_t)k * 4 : 0;
-        InSlot& si = p->in_slots[p->next_in];
-        OutSlot& so = p->out_slots[p->next_out];
+        Chunk c;
+        c.valid = true;
+        c.slot = p->next_in;
+        c.ggml_type = ggml_type;
+        c.src_type = src_type;
+        c.n = std::min(rows_per_chunk, n_rows - r0);
+        c.k = k;
+        c.in_row = in_row;
+        c.nin = (size_t)(c.n * in_row);
+        c.nout = (size_t)(c.n * out_row);
+        c.nqw = use_qw ? (size_t)k * 4 : 0;
+        c.fd = fd;
+        c.out_off = out_offset + r0 * out_row;
+        InSlot& si = p->in_slots[c.slot];
         p->next_in = (p->next_in + 1) % p->in_slots.size();
-        p->next_out = (p->next_out + 1) % p->out_slots.size();
+        // the pending chunk holds the slot before this one, so this slot's last
+        // chunk is queued: wait for its upload (in_pin) and, if the device
+        // buffers must grow, for the kernel that read them
         if (si.used) {
-            // in_pin: its H2D is done; the device buffers: if they must grow,
-            // the kernel that read them is done
             if ((e = hipEventSynchronize(si.h2d)) != hipSuccess) return p->hip_fail(e, "H2D");
-            if ((si.x_dev.n < nin || si.qw_dev.n < nqw) && (e = hipEventSynchronize(si.kern)) != hipSuccess)
+            if ((si.x_dev.n < c.nin || si.qw_dev.n < c.nqw) && (e = hipEventSynchronize(si.kern)) != hipSuccess)
                 return p->hip_fail(e, "kernel");
         }
-        if (so.used) {
-            // out_pin: its write is done; out_dev: if it must grow, its D2H is done
-            p->writer->wait(so.write_seq);
-            if (int rc = p->check_writer()) return rc;
-            if (so.out_dev.n < nout && (e = hipEventSynchronize(so.d2h)) != hipSuccess)
-                return p->hip_fail(e, "D2H");
-        }
-        if (!si.in_pin.grow(nin) || !si.qw_pin.grow(nqw) || !si.x_dev.grow(nin) || !si.qw_dev.grow(nqw) ||
-            !so.out_pin.grow(nout) || !so.out_dev.grow(nout)) {
+        if (!si.in_pin.grow(c.nin) || !si.qw_pin.grow(c.nqw) || !si.x_dev.grow(c.nin) || !si.qw_dev.grow(c.nqw)) {
             if (p->err.empty()) p->err = "out of memory staging a chunk";
-            return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)n,
+            return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)c.n,
                         (long long)in_row);
         }
-        // rows -> pinned, in parts of at least kCopyPart bytes
+        if (c.nqw) std::memcpy(si.qw_pin.p, imatrix, c.nqw);
+        // the pending chunk's rows are in place once the pool is idle
+        if (int rc = wait_reads(p)) return rc;
+        // this chunk's rows -> pinned, on the pool, in parts of at least kCopyPart bytes
         const size_t from = (size_t)(r0 * in_row);
         char* to = static_cast<char*>(si.in_pin.p);
-        const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), nin / kCopyPart));
+        const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), c.nin / kCopyPart));
         std::vector<std::function<void()>> tasks;
-        std::atomic<int> read_err{0};
+        std::atomic<int>* read_err = &p->read_err;
         for (size_t i = 0; i < parts; i++) {
-            const size_t a = nin * i / parts, b = nin * (i + 1) / parts;
-            tasks.emplace_back([&src, &read_err, from, to, a, b] {
-                if (const int e = copy_rows(src, from + a, to + a, b - a)) read_err.store(e);
+            const size_t a = c.nin * i / parts, b = c.nin * (i + 1) / parts;
+            tasks.emplace_back([src, read_err, from, to, a, b] {
+                if (const int re = copy_rows(src, from + a, to + a, b - a)) read_err->store(re);
             });
         }
-        p->pool->run(tasks);
-        if (const int re = read_err.load()) {
-            if (p->err.empty()) p->err = std::string("reading the input rows failed: ") + std::strerror(re);
-            return fail(QS_EIO, "%s", p->err.c_str());
-        }
-        if (nqw) std::memcpy(si.qw_pin.p, imatrix, nqw);
-
-        // the upload overwrites x_dev / qw_dev once the kernel that read them is done
-        if (si.used && (e = hipStreamWaitEvent(p->h2d, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(si.x_dev.p, si.in_pin.p, nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
-            return p->hip_fail(e, "H2D");
-        if (nqw && (e = hipMemcpyAsync(si.qw_dev.p, si.qw_pin.p, nqw, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
-            return p->hip_fail(e, "H2D");
-        if ((e = hipEventRecord(si.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
-        // the kernel writes out_dev once the D2H that read it is done
-        hipStream_t cs = p->compute[p->launches++ & 1];
-        if ((e = hipStreamWaitEvent(cs, si.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if (so.used && (e = hipStreamWaitEvent(cs, so.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        const int rc = qs_quantize(ggml_type, src_type, si.x_dev.p, n, k, in_row,
-                                   nqw ? static_cast<const float*>(si.qw_dev.p) : nullptr, so.out_dev.p,
-                                   (int64_t)nout, cs);
-        if (rc) {
-            if (p->err.empty()) p->err = "quantizer launch failed";
-            return rc;
-        }
-        if ((e = hipEventRecord(si.kern, cs)) != hipSuccess) return p->hip_fail(e, "event");
-        if ((e = hipStreamWaitEvent(p->d2h, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-        if ((e = hipMemcpyAsync(so.out_pin.p, so.out_dev.p, nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
-            return p->hip_fail(e, "D2H");
-        if ((e = hipEventRecord(so.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
-        si.used = so.used = true;
-        so.write_seq = p->writer->push({so.d2h, so.out_pin.p, nout, fd, out_offset + r0 * out_row});
+        p->pool->submit(tasks);
+        // while the pool reads: the previous chunk's launch
+        const int rc = launch_pending(p);
+        p->pending = c;
+        if (rc) return rc;
     }
     return 0;
 }
@@ -496,20 +577,24 @@ int qs_pipeline_write(qs_pipeline* p, const void* src, int64_t nbytes, int fd, i
 int qs_pipeline_finish(qs_pipeline* p) {
     qs_host::clear_error();
     if (!p) return fail(QS_EINVAL, "null pipeline");
-    p->writer->drain();
     hipError_t e = hipSetDevice(p->device);
+    // the last chunk's launch (its read may still run), then everything it queued
+    const int prc = e == hipSuccess ? flush_pending(p) : p->hip_fail(e, "hipSetDevice");
+    p->writer->drain();
     if (e == hipSuccess) e = hipStreamSynchronize(p->h2d);
     if (e == hipSuccess) e = hipStreamSynchronize(p->d2h);
     for (hipStream_t cs : p->compute)
         if (e == hipSuccess) e = hipStreamSynchronize(cs);
     if (e != hipSuccess) return p->hip_fail(e, "device work failed");
+    if (prc) return prc;
     return p->check_writer();
 }
 
 void qs_pipeline_destroy(qs_pipeline* p) {
     if (!p) return;
-    if (p->writer) p->writer->drain();
     (void)hipSetDevice(p->device);
+    if (p->pool && p->writer) (void)flush_pending(p);
+    if (p->writer) p->writer->drain();
     if (p->h2d) (void)hipStreamSynchronize(p->h2d);
     if (p->d2h) (void)hipStreamSynchronize(p->d2h);
     for (hipStream_t cs : p->compute)

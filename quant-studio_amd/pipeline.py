@@ -2,9 +2,9 @@
 
 The staging itself is native (qs_pipeline_* in libqs_hip.so): a ring of
 pinned slots, a thread pool that reads each chunk's rows from the input file
-(pread) into its slot, H2D and D2H on copy streams, kernels on two compute
-streams, and a writer thread that pwrite()s each chunk at its own file offset
-once its D2H event has fired. It replaces
+(pread) into its slot one chunk ahead of the launches, H2D and D2H on copy
+streams, kernels on two compute streams, and a writer thread that pwrite()s
+each chunk at its own file offset once its D2H event has fired. It replaces
 the reference's CudaPipeline, OutputWriter and copy_tensor
 (quant-studio.py:103-131, :148-213, :235-241). Python keeps what the
 reference keeps in Python: the GGUF header, tensor order and offsets, the type
@@ -142,7 +142,9 @@ class NativePipeline:
         the output file, staged in chunks of at most rows_per_chunk rows and
         STAGE_BYTES input bytes; returns its bytes. With src_fd (the input
         file's descriptor, t read from it) the rows are read with pread at
-        t.file_offset, else copied from t's mapping."""
+        t.file_offset, else copied from t's mapping. The last chunk's rows may
+        still be being read when this returns: the descriptor and the rows
+        stay in use until finish()."""
         rows = t.rows()
         n_rows = rows.shape[0]
         k = t.ne[0]
@@ -157,6 +159,7 @@ class NativePipeline:
                                                        int(src_fd), int(t.file_offset), n_rows, k, qptr,
                                                        int(rows_per_chunk), self.fd, int(offset)))
         else:
+            self._keep.append(rows)
             self._check(self.L.qs_pipeline_quantize(self.h, int(ggml_type), SRC_IDS[t.ggml_type],
                                                     rows.ctypes.data, n_rows, k, qptr, int(rows_per_chunk),
                                                     self.fd, int(offset)))

@@ -189,7 +189,8 @@ def test_pipeline_reads_rows_from_the_file(tmp_path):
     """qs_pipeline_quantize_fd (rows read with pread at a file offset) writes
     the oracle's bytes for any chunking, bf16 and f32 rows at unaligned file
     offsets alike; a tensor that runs past the end of the file fails with
-    QS_EIO naming the read, and an invalid descriptor or offset is refused."""
+    QS_EIO naming the read (no later than qs_pipeline_finish), and an invalid
+    descriptor or offset is refused."""
     import ctypes
     import os
     qs = importlib.import_module("quant-studio_amd")
@@ -223,9 +224,12 @@ def test_pipeline_reads_rows_from_the_file(tmp_path):
         fd = os.open(tmp_path / "short.bin", os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
         try:
             with pl.NativePipeline(0, fd) as p:
-                # 4 more rows than the file holds after the bf16 block
+                # 4 more rows than the file holds after the bf16 block: the
+                # read fails on the pool, reported by the call or by finish
                 rc = p.L.qs_pipeline_quantize_fd(p.h, int(GT.Q4_K), 30, sfd, lead + x.nbytes, 33, 512,
                                                  None, 64, fd, 0)
+                if rc == 0:
+                    rc = p.L.qs_pipeline_finish(p.h)
                 assert rc == -5 and "reading the input rows failed" in qs.last_error()
                 assert p.L.qs_pipeline_quantize_fd(p.h, int(GT.Q4_K), 30, -1, 0, 1, 512, None, 1,
                                                    fd, 0) == -22
@@ -235,6 +239,58 @@ def test_pipeline_reads_rows_from_the_file(tmp_path):
             os.close(fd)
     finally:
         os.close(sfd)
+
+
+def test_pipeline_tensors_back_to_back(tmp_path):
+    """Tensors of other widths, types and sources queued back to back: each
+    queue call leaves its last chunk pending (its rows still being read) and
+    the next call launches it, input slots are reused by rows of other widths
+    and imatrices of other lengths, rows come from the file (bf16, pread) and
+    from host memory (f32) in turn; every tensor's bytes are the oracle's."""
+    import os
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    rng = np.random.default_rng(11)
+    # (type, k, rows, rows per chunk)
+    specs = [(GT.Q4_K, 512, 23, 5), (GT.IQ4_XS, 1024, 9, 4), (GT.Q6_K, 256, 40, 40), (GT.Q4_0, 2048, 7, 3),
+             (GT.Q3_K, 768, 13, 1), (GT.Q4_K, 256, 64, 17), (GT.IQ3_XXS, 4096, 3, 2)]
+    src = tmp_path / "rows.bin"
+    blob, tensors, want = bytearray(b"\0" * 11), [], []
+    for i, (gt, k, n, rpc) in enumerate(specs):
+        x = (rng.normal(size=(n, k)) * 0.02).astype(np.float32)
+        qw = rng.lognormal(size=k).astype(np.float32)
+        if i % 2 == 0:      # bf16 rows in the file at an odd offset
+            raw = (x.view(np.uint32) >> 16).astype(np.uint16)
+            xf = (raw.astype(np.uint32) << 16).view(np.float32)
+            info = io.TensorInfo(f"t{i}", (k, n), GT.BF16, 0, raw.nbytes, raw.view(np.uint8).reshape(-1), len(blob))
+            blob += raw.tobytes()
+        else:               # f32 rows from host memory
+            xf = x
+            info = io.TensorInfo(f"t{i}", (k, n), GT.F32, 0, x.nbytes, x.view(np.uint8).reshape(-1))
+        name = gt.name.lower()
+        want.append(oracle.quantize(name, xf, None if gt == GT.Q4_0 else qw))
+        tensors.append((info, gt, qw, rpc))
+    src.write_bytes(bytes(blob))
+    out = tmp_path / "o.bin"
+    sfd = os.open(src, os.O_RDONLY)
+    fd = os.open(out, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+    try:
+        with pl.NativePipeline(0, fd) as p:
+            off = 0
+            for info, gt, qw, rpc in tensors:
+                print(f"queue {gt.name} {info.ne} rows/chunk {rpc}", flush=True)
+                off += p.quantize_tensor(info, int(gt), qw, rpc, off, qs.row_bytes(int(gt), info.ne[0]),
+                                         sfd if info.ggml_type == GT.BF16 else -1)
+            p.finish()
+    finally:
+        os.close(fd)
+        os.close(sfd)
+    got, off = out.read_bytes(), 0
+    for (info, gt, _, _), ref in zip(tensors, want):
+        part = np.frombuffer(got[off:off + ref.nbytes], np.uint8).reshape(ref.shape)
+        assert np.array_equal(part, ref), (gt.name, info.ne)
+        off += ref.nbytes
+    assert off == len(got)
 
 
 def test_pipeline_made_on_another_thread(tmp_path):
