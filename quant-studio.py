@@ -14,4 +14,13 @@ from pathlib import Path
 sys.path.insert(0, str(Path(__file__).resolve().parent))
 
 if __name__ == "__main__":
-    sys.exit(importlib.import_module("quant-studio_amd.cli").main())
+    # the device's initialisation starts first, on a thread of its own; the
+    # command line's imports, parsing and planning then overlap it
+    early = importlib.import_module("quant-studio_amd.pipeline_start").early_start(sys.argv[1:])
+    try:
+        cli = importlib.import_module("quant-studio_amd.cli")
+    except BaseException:
+        if early is not None:
+            early.close()
+        raise
+    sys.exit(cli.main(early=early))

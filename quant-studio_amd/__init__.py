@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import sys
+import threading
 from pathlib import Path
 
 from .gguf_types import GGMLQuantizationType, LlamaFileType
@@ -72,8 +73,21 @@ def _bind_torch_hip_runtime() -> None:
             return
 
 
+_lib_lock = threading.Lock()
+
+
 def library() -> ctypes.CDLL:
-    """Load libqs_hip.so (built in-tree by build.py); raises if it is missing."""
+    """Load libqs_hip.so (built in-tree by build.py); raises if it is missing.
+    Thread-safe: the command line may load it from a pipeline-creating thread
+    while the main thread gets to it too."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        return _load_library()
+
+
+def _load_library() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not LIB_PATH.exists():

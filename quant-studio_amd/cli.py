@@ -349,19 +349,24 @@ def preallocate(fd: int, size: int) -> bool:
     return size > 0 and fn(fd, 0, 0, size) == 0
 
 
-def start_device(req: Request):
-    """Starts the native pipeline's creation on a thread of its own (a
-    PipelineStart) once the request is parsed, so the device's initialisation
-    overlaps loading the imatrix, parsing the input and planning the tensors;
-    None when the requested device is absent. Which device is used, and every
-    error, is still decided by write_output in the reference's order (its
-    pipeline is created after the plan, quant-studio.py:445-449)."""
-    from .pipeline import PipelineStart, device_count
+def start_device(req: Request, early=None):
+    """The native pipeline's creation on a thread of its own (a
+    PipelineStart), so the device's initialisation overlaps loading the
+    imatrix, parsing the input and planning the tensors: `early` (started by
+    the entry script from argv) if it is for the requested device, else one
+    started now; None for a dry run. Which device is used, and every error, is
+    still decided by write_output in the reference's order (its pipeline is
+    created after the plan, quant-studio.py:445-449)."""
+    from .pipeline_start import PipelineStart
     try:
-        dev = int(req.device.split(":", 1)[1]) if ":" in req.device else 0
+        dev = None if req.dry_run else (int(req.device.split(":", 1)[1]) if ":" in req.device else 0)
     except ValueError:
-        return None
-    return PipelineStart(dev) if 0 <= dev < device_count() else None
+        dev = None
+    if early is not None and early.device == dev:
+        return early
+    if early is not None:
+        early.close()
+    return None if dev is None or dev < 0 else PipelineStart(dev)
 
 
 def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: dict,
@@ -429,13 +434,16 @@ def write_output(req: Request, reader: GGUFReader, steps: list[Step], imatrix: d
           f"({total_out / max(total_in, 1) * 100:.1f}%)")
 
 
-def main(argv: list[str] | None = None) -> int:
-    req = parse_request(argv)
-    device_shown = "rocm" if req.device not in ("cpu", "mps") else f"{req.device} (on rocm)"
-    print(f"quant-studio: {req.src} -> {req.dst} [{req.option.name}] device={device_shown} "
-          f"mem={req.mem_text} sqrt-rounding={req.sqrt_rounding}")
-    start = None if req.dry_run else start_device(req)
+def main(argv: list[str] | None = None, early=None) -> int:
+    """The command line; `early` is a PipelineStart the entry script began
+    from argv before importing this module (pipeline_start.early_start)."""
+    start = early
     try:
+        req = parse_request(argv)
+        device_shown = "rocm" if req.device not in ("cpu", "mps") else f"{req.device} (on rocm)"
+        print(f"quant-studio: {req.src} -> {req.dst} [{req.option.name}] device={device_shown} "
+              f"mem={req.mem_text} sqrt-rounding={req.sqrt_rounding}")
+        start = start_device(req, early)
         imatrix: dict[str, np.ndarray] = {}
         if req.imatrix is not None:
             imatrix = load_imatrix(req.imatrix)

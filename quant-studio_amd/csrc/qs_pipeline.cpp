@@ -5,26 +5,25 @@
 // Replaces the reference's CudaPipeline (quant-studio.py:148-213),
 // OutputWriter (:103-131) and copy_tensor (:235-241):
 //   - a ring of input slots (pinned rows and imatrix, their device copies) and
-//     a deeper ring of output slots (device output, pinned copy), so the host
-//     copy of chunk i+2, the H2D of chunk i+1, the kernel of chunk i and the
-//     D2H and file write of earlier chunks overlap, and a writer a few chunks
+//     a deeper ring of output slots (pinned host memory the kernel writes
+//     directly), so the host read of chunk i+1, the H2D and kernel of chunk i
+//     and the file writes of earlier chunks overlap, and a writer a few chunks
 //     behind does not hold back the next uploads;
 //   - the read (or copy) into pinned memory of a chunk split over a pool of
 //     threads (one thread caps the pipeline well below the PCIe rate), and
 //     run one chunk ahead of the launches: a queue call starts the pool on
-//     its chunk, then queues the previous chunk's upload, kernel and download
-//     while the pool reads, and leaves its own last chunk pending for the
-//     next call or qs_pipeline_finish, so reads overlap the launches and the
-//     caller's work between tensors;
-//   - H2D and D2H on two copy streams (so the next chunk's upload never queues
-//     behind this chunk's download, which waits for its kernel), kernels on
-//     two compute streams taken in turn, all ordered by per-slot events; the
-//     calling thread never waits on the GPU except for a slot. Consecutive
-//     kernels may overlap: the next chunk's waves fill the GPU while the last
-//     waves of this one drain (a fixed ~0.36 wave-lifetime per launch, ~10%
-//     of a Q4_K + imatrix launch on a 9728x2560 tensor);
+//     its chunk, then queues the previous chunk's upload and kernel while the
+//     pool reads, and leaves its own last chunk pending for the next call or
+//     qs_pipeline_finish, so reads overlap the launches and the caller's work
+//     between tensors;
+//   - uploads on a copy stream, kernels on two compute streams taken in turn,
+//     ordered by per-slot events; the calling thread never waits on the GPU
+//     except for a slot. Consecutive kernels may overlap: the next chunk's
+//     waves fill the GPU while the last waves of this one drain (a fixed
+//     ~0.36 wave-lifetime per launch, ~10% of a Q4_K + imatrix launch on a
+//     9728x2560 tensor);
 //   - rows handed to the kernel in their stored type (no f32 upcast pass);
-//   - one writer thread that waits on each chunk's D2H event and writes the
+//   - one writer thread that waits on each chunk's kernel event and writes the
 //     chunk at its own offset, so the output never depends on the chunking.
 #include <hip/hip_runtime.h>
 #include <unistd.h>
@@ -201,13 +200,14 @@ inline size_t alloc_size(size_t want) {
 struct PinnedBuf {
     void* p = nullptr;
     size_t n = 0;
+    unsigned flags = hipHostMallocDefault;
     bool grow(size_t want) {
         if (n >= want) return true;
         if (p) (void)hipHostFree(p);
         p = nullptr;
         n = 0;
         want = alloc_size(want);
-        if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) return false;
+        if (hipHostMalloc(&p, want, flags) != hipSuccess) return false;
         n = want;
         return true;
     }
@@ -247,13 +247,16 @@ struct InSlot {
     bool used = false;            // events recorded at least once
 };
 
-// Output ring: the kernel's device output and its pinned copy for the writer.
-// Deeper than the input ring, so a writer running a few chunks behind the GPU
-// does not stop the calling thread from staging the next inputs.
+// Output ring: pinned host memory (coherent: the device's stores go over the
+// bus to host memory, not into its caches) that the kernel writes directly,
+// so no download is queued: the chunk's output is a few MB against 16 MiB of
+// input, and a download per chunk cost a copy kernel on the device and a
+// slow runtime call on the host. Deeper than the input ring, so a writer
+// running a few chunks behind the GPU does not stop the calling thread from
+// staging the next inputs.
 struct OutSlot {
-    DevBuf out_dev;
     PinnedBuf out_pin;
-    hipEvent_t d2h = nullptr;     // out_pin holds the chunk; out_dev is free
+    hipEvent_t ready = nullptr;   // the kernel that writes out_pin is done
     bool used = false;
     uint64_t write_seq = 0;       // writer job that reads out_pin
 };
@@ -269,8 +272,8 @@ int elem_size(int src_type) {
 
 }  // namespace
 
-// A chunk whose rows are being read into its input slot and whose upload,
-// kernel and download are not queued yet.
+// A chunk whose rows are being read into its input slot and whose upload and
+// kernel are not queued yet.
 struct Chunk {
     bool valid = false;
     size_t slot = 0;          // input slot
@@ -283,7 +286,7 @@ struct Chunk {
 
 struct qs_pipeline {
     int device = 0;
-    hipStream_t h2d = nullptr, d2h = nullptr, compute[2] = {nullptr, nullptr};
+    hipStream_t h2d = nullptr, compute[2] = {nullptr, nullptr};
     std::vector<InSlot> in_slots;
     std::vector<OutSlot> out_slots;
     size_t next_in = 0, next_out = 0;
@@ -359,7 +362,6 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline*
     auto p = std::make_unique<qs_pipeline>();
     p->device = device;
     if ((e = hipStreamCreateWithFlags(&p->h2d, hipStreamNonBlocking)) != hipSuccess ||
-        (e = hipStreamCreateWithFlags(&p->d2h, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipStreamCreateWithFlags(&p->compute[0], hipStreamNonBlocking)) != hipSuccess ||
         (e = hipStreamCreateWithFlags(&p->compute[1], hipStreamNonBlocking)) != hipSuccess) {
         qs_pipeline_destroy(p.release());
@@ -375,7 +377,8 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline*
         }
     }
     for (auto& s : p->out_slots) {
-        if ((e = hipEventCreateWithFlags(&s.d2h, hipEventDisableTiming)) != hipSuccess) {
+        s.out_pin.flags = hipHostMallocCoherent;
+        if ((e = hipEventCreateWithFlags(&s.ready, hipEventDisableTiming)) != hipSuccess) {
             qs_pipeline_destroy(p.release());
             return fail(QS_EIO, "event creation failed: %s", hipGetErrorString(e));
         }
@@ -409,6 +412,24 @@ int qs_pipeline_quantize_fd(qs_pipeline* p, int ggml_type, int src_type, int src
 
 }  // extern "C"
 
+// Touch every page of a newly allocated pinned buffer from the pool's threads
+// (and wait). The host mapping of hipHostMalloc memory is filled in on first
+// access, a page fault per few pages: the first pread into a 16 MiB input
+// slot, or the writer's first pwrite from a 6 MiB output slot, took ~2.5 ms
+// longer than later ones on the MI355X machine's host, on the pipeline's
+// critical path; touched in parallel the faults cost a fraction of that.
+static void touch_pages(qs_pipeline* p, void* buf, size_t n) {
+    const size_t parts = std::max<size_t>(1, std::min<size_t>((size_t)p->pool->size(), n / kCopyPart));
+    std::vector<std::function<void()>> tasks;
+    char* b = static_cast<char*>(buf);
+    for (size_t i = 0; i < parts; i++) {
+        const size_t lo = n * i / parts, hi = n * (i + 1) / parts;
+        tasks.emplace_back([b, lo, hi] { std::memset(b + lo, 0, hi - lo); });
+    }
+    p->pool->submit(tasks);
+    p->pool->wait();
+}
+
 // Wait for the pool's reads (the pending chunk's) and report a failed one.
 static int wait_reads(qs_pipeline* p) {
     p->pool->wait();
@@ -421,7 +442,7 @@ static int wait_reads(qs_pipeline* p) {
 }
 
 // Queue the pending chunk (its rows are in its input slot): upload, kernel on
-// the next compute stream, download into an output slot, write job.
+// the next compute stream writing into an output slot, write job.
 static int launch_pending(qs_pipeline* p) {
     if (!p->pending.valid) return 0;
     const Chunk c = p->pending;
@@ -431,16 +452,17 @@ static int launch_pending(qs_pipeline* p) {
     p->next_out = (p->next_out + 1) % p->out_slots.size();
     hipError_t e;
     if (so.used) {
-        // out_pin: its write is done; out_dev: if it must grow, its D2H is done
+        // out_pin is free once its write is done (the writer waited for the
+        // kernel that wrote it)
         p->writer->wait(so.write_seq);
         if (int rc = p->check_writer()) return rc;
-        if (so.out_dev.n < c.nout && (e = hipEventSynchronize(so.d2h)) != hipSuccess)
-            return p->hip_fail(e, "D2H");
     }
-    if (!so.out_pin.grow(c.nout) || !so.out_dev.grow(c.nout)) {
+    const size_t out_had = so.out_pin.n;
+    if (!so.out_pin.grow(c.nout)) {
         if (p->err.empty()) p->err = "out of memory staging a chunk";
         return fail(QS_EIO, "out of memory staging the output of a chunk of %lld rows", (long long)c.n);
     }
+    if (so.out_pin.n != out_had) touch_pages(p, so.out_pin.p, so.out_pin.n);
     // the upload overwrites x_dev / qw_dev once the kernel that read them is done
     if (si.used && (e = hipStreamWaitEvent(p->h2d, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
     if ((e = hipMemcpyAsync(si.x_dev.p, si.in_pin.p, c.nin, hipMemcpyHostToDevice, p->h2d)) != hipSuccess)
@@ -449,24 +471,19 @@ static int launch_pending(qs_pipeline* p) {
         return p->hip_fail(e, "H2D");
     if ((e = hipEventRecord(si.h2d, p->h2d)) != hipSuccess) return p->hip_fail(e, "event");
     si.used = true;
-    // the kernel writes out_dev once the D2H that read it is done
     hipStream_t cs = p->compute[p->launches++ & 1];
     if ((e = hipStreamWaitEvent(cs, si.h2d, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-    if (so.used && (e = hipStreamWaitEvent(cs, so.d2h, 0)) != hipSuccess) return p->hip_fail(e, "wait");
     const int rc = qs_quantize(c.ggml_type, c.src_type, si.x_dev.p, c.n, c.k, c.in_row,
-                               c.nqw ? static_cast<const float*>(si.qw_dev.p) : nullptr, so.out_dev.p,
+                               c.nqw ? static_cast<const float*>(si.qw_dev.p) : nullptr, so.out_pin.p,
                                (int64_t)c.nout, cs);
     if (rc) {
         if (p->err.empty()) p->err = "quantizer launch failed";
         return rc;
     }
     if ((e = hipEventRecord(si.kern, cs)) != hipSuccess) return p->hip_fail(e, "event");
-    if ((e = hipStreamWaitEvent(p->d2h, si.kern, 0)) != hipSuccess) return p->hip_fail(e, "wait");
-    if ((e = hipMemcpyAsync(so.out_pin.p, so.out_dev.p, c.nout, hipMemcpyDeviceToHost, p->d2h)) != hipSuccess)
-        return p->hip_fail(e, "D2H");
-    if ((e = hipEventRecord(so.d2h, p->d2h)) != hipSuccess) return p->hip_fail(e, "event");
+    if ((e = hipEventRecord(so.ready, cs)) != hipSuccess) return p->hip_fail(e, "event");
     so.used = true;
-    so.write_seq = p->writer->push({so.d2h, so.out_pin.p, c.nout, c.fd, c.out_off});
+    so.write_seq = p->writer->push({so.ready, so.out_pin.p, c.nout, c.fd, c.out_off});
     return 0;
 }
 
@@ -532,11 +549,13 @@ static int pipeline_quantize(qs_pipeline* p, int ggml_type, int src_type, const 
             if ((si.x_dev.n < c.nin || si.qw_dev.n < c.nqw) && (e = hipEventSynchronize(si.kern)) != hipSuccess)
                 return p->hip_fail(e, "kernel");
         }
+        const size_t in_had = si.in_pin.n;
         if (!si.in_pin.grow(c.nin) || !si.qw_pin.grow(c.nqw) || !si.x_dev.grow(c.nin) || !si.qw_dev.grow(c.nqw)) {
             if (p->err.empty()) p->err = "out of memory staging a chunk";
             return fail(QS_EIO, "out of memory staging a chunk of %lld rows x %lld bytes", (long long)c.n,
                         (long long)in_row);
         }
+        if (si.in_pin.n != in_had) touch_pages(p, si.in_pin.p, si.in_pin.n);
         if (c.nqw) std::memcpy(si.qw_pin.p, imatrix, c.nqw);
         // the pending chunk's rows are in place once the pool is idle
         if (int rc = wait_reads(p)) return rc;
@@ -582,7 +601,6 @@ int qs_pipeline_finish(qs_pipeline* p) {
     const int prc = e == hipSuccess ? flush_pending(p) : p->hip_fail(e, "hipSetDevice");
     p->writer->drain();
     if (e == hipSuccess) e = hipStreamSynchronize(p->h2d);
-    if (e == hipSuccess) e = hipStreamSynchronize(p->d2h);
     for (hipStream_t cs : p->compute)
         if (e == hipSuccess) e = hipStreamSynchronize(cs);
     if (e != hipSuccess) return p->hip_fail(e, "device work failed");
@@ -596,7 +614,6 @@ void qs_pipeline_destroy(qs_pipeline* p) {
     if (p->pool && p->writer) (void)flush_pending(p);
     if (p->writer) p->writer->drain();
     if (p->h2d) (void)hipStreamSynchronize(p->h2d);
-    if (p->d2h) (void)hipStreamSynchronize(p->d2h);
     for (hipStream_t cs : p->compute)
         if (cs) (void)hipStreamSynchronize(cs);
     p->writer.reset();
@@ -611,11 +628,9 @@ void qs_pipeline_destroy(qs_pipeline* p) {
     }
     for (auto& s : p->out_slots) {
         s.out_pin.release();
-        s.out_dev.release();
-        if (s.d2h) (void)hipEventDestroy(s.d2h);
+        if (s.ready) (void)hipEventDestroy(s.ready);
     }
     if (p->h2d) (void)hipStreamDestroy(p->h2d);
-    if (p->d2h) (void)hipStreamDestroy(p->d2h);
     for (hipStream_t cs : p->compute)
         if (cs) (void)hipStreamDestroy(cs);
     delete p;

@@ -23,6 +23,7 @@ import numpy as np
 from . import library, last_error
 from .gguf_io import TensorInfo
 from .gguf_types import GGMLQuantizationType as GT
+from .pipeline_start import PipelineStart  # noqa: F401  (created before numpy is imported)
 
 # source ids of the C ABI (QS_SRC_*)
 SRC_IDS = {GT.F32: 0, GT.F16: 1, GT.BF16: 30}
@@ -187,41 +188,3 @@ class NativePipeline:
 
     def __exit__(self, *exc):
         self.close()
-
-
-class PipelineStart:
-    """qs_pipeline_create on a thread of its own. The thread makes just that C
-    call, which releases the GIL, so the device's initialisation (its first
-    stream creation sets up the device's queues: ~0.08 s on the MI355X) runs
-    while the calling thread goes on with Python work. take() joins it and
-    returns the NativePipeline, or None if the creation failed (the caller
-    then creates one itself and sees the error on its own thread)."""
-
-    def __init__(self, device: int, slots: int = 3, copy_threads: int | None = None):
-        import threading
-        self.device = int(device)
-        self._L = library()
-        self._h = ctypes.c_void_p()
-        self._rc: int | None = None
-        create = self._L.qs_pipeline_create
-        args = (self.device, int(slots), int(copy_threads or default_copy_threads()), ctypes.byref(self._h))
-
-        def run() -> None:
-            self._rc = create(*args)
-
-        self._thread = threading.Thread(target=run, name="qs-pipeline-create", daemon=True)
-        self._thread.start()
-
-    def take(self, fd: int) -> NativePipeline | None:
-        self._thread.join()
-        if self._rc != 0 or not self._h.value:
-            return None
-        h, self._h = self._h, ctypes.c_void_p()
-        return NativePipeline(self.device, fd, handle=h)
-
-    def close(self) -> None:
-        """Release a pipeline that was not taken."""
-        self._thread.join()
-        if self._rc == 0 and self._h.value:
-            self._L.qs_pipeline_destroy(self._h)
-            self._h = ctypes.c_void_p()
