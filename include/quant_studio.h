@@ -177,7 +177,7 @@ int qs_pipeline_create(int device, int n_slots, int n_copy_threads, qs_pipeline 
  * with the host imatrix (k floats or NULL; as qs_quantize; copied before the
  * call returns), the output rows written contiguously at out_offset of fd.
  * The rows of each chunk are read by the pipeline's threads while the
- * previous chunk's upload, kernel and download are queued; the call returns
+ * previous chunk's upload and kernel are queued; the call returns
  * with its last chunk still being read (that chunk is queued by the next call
  * on the pipeline or by qs_pipeline_finish), and blocks only while all slots
  * are busy. At most 2^34 values per tensor (QS_EINVAL otherwise). One

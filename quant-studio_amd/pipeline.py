@@ -2,9 +2,10 @@
 
 The staging itself is native (qs_pipeline_* in libqs_hip.so): a ring of
 pinned slots, a thread pool that reads each chunk's rows from the input file
-(pread) into its slot one chunk ahead of the launches, H2D and D2H on copy
-streams, kernels on two compute streams, and a writer thread that pwrite()s
-each chunk at its own file offset once its D2H event has fired. It replaces
+(pread) into its slot one chunk ahead of the launches, uploads on a copy
+stream, kernels on two compute streams writing each chunk's output into a
+pinned host slot, and a writer thread that pwrite()s each chunk at its own
+file offset once its kernel has finished. It replaces
 the reference's CudaPipeline, OutputWriter and copy_tensor
 (quant-studio.py:103-131, :148-213, :235-241). Python keeps what the
 reference keeps in Python: the GGUF header, tensor order and offsets, the type
@@ -103,13 +104,13 @@ def device_count() -> int:
 # Input bytes per staged chunk. --mem bounds a chunk (the reference's budget
 # per row chunk, quant-studio.py:457); the pipeline stages at most this much
 # per chunk within it. The output does not depend on the chunking, and with
-# chunks of this size the read, H2D, kernel, D2H and write of
+# chunks of this size the read, upload, kernel and write of
 # consecutive chunks overlap inside every tensor instead of across whole
 # tensors, and the pinned slots stay small. Measured on the synthetic
-# 4B-class model, warm (process wall, one MI355X): IQ2_XXS 0.77 s with whole
-# tensors per chunk (--mem 4G) -> 0.61 s at 16 MiB (8 MiB 0.62, 32 MiB 0.62,
-# 64 MiB 0.67, 128 MiB 0.73); Q4_K_M 0.74 -> 0.49 s; IQ3_XXS 0.74 -> 0.60 s
-# (at 32 MiB); IQ2_S 0.89 -> 0.76 s (at 32 MiB).
+# 4B-class model, warm (process wall, one MI355X, when this size was chosen):
+# IQ2_XXS 0.77 s with whole tensors per chunk (--mem 4G) -> 0.61 s at 16 MiB
+# (8 MiB 0.62, 32 MiB 0.62, 64 MiB 0.67, 128 MiB 0.73); Q4_K_M 0.74 -> 0.49
+# s; IQ3_XXS 0.74 -> 0.60 s (at 32 MiB); IQ2_S 0.89 -> 0.76 s (at 32 MiB).
 STAGE_BYTES = 16 << 20
 
 
