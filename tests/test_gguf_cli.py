@@ -312,3 +312,19 @@ def test_requested_device_from_argv():
     assert rd(["in.gguf", "out.gguf", "Q4_K_M", "--device", "cuda:x"]) is None
     assert rd(["in.gguf", "out.gguf", "Q4_K_M", "--dry-run"]) is None
     assert rd(["--help"]) is None and rd([]) is None
+
+
+def test_early_start_without_a_device():
+    """An early start for a device that is not there (no GPU here) ends on
+    its own: take() hands back no pipeline, so the command line creates one
+    itself and reports the missing device in the reference's words, and
+    close() releases nothing."""
+    ps = importlib.import_module("quant-studio_amd.pipeline_start")
+    qs = importlib.import_module("quant-studio_amd")
+    if qs.library().qs_device_count() > 0:
+        pytest.skip("a ROCm device is visible")
+    start = ps.early_start(["in.gguf", "out.gguf", "Q4_K_M"])
+    assert start is not None and start.device == 0
+    assert start.take(1) is None
+    start.close()
+    assert ps.early_start(["in.gguf", "out.gguf", "Q4_K_M", "--dry-run"]) is None
