@@ -270,8 +270,6 @@ int elem_size(int src_type) {
     }
 }
 
-}  // namespace
-
 // A chunk whose rows are being read into its input slot and whose upload and
 // kernel are not queued yet.
 struct Chunk {
@@ -283,6 +281,8 @@ struct Chunk {
     int fd = -1;
     int64_t out_off = 0;
 };
+
+}  // namespace
 
 struct qs_pipeline {
     int device = 0;
