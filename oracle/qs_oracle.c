@@ -1,6 +1,6 @@
 /*
  * CPU oracle for the GGUF block quantizers -- TEST INFRASTRUCTURE ONLY
- * (parity checker for tests/, smoke() and the CPU-baseline leg of bench.py;
+ * (the expected bytes for tests/, smoke() and the CPU-baseline leg of bench.py;
  * never linked into the product library).
  *
  * Restates the reference's eager torch CPU path type by type. Conventions that
