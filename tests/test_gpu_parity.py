@@ -163,6 +163,37 @@ def test_oracle_parity_random(qs, dev, qtype, imat):
     assert same.all(), f"{int((~same).sum())}/{same.size} blocks differ"
 
 
+@pytest.mark.parametrize("qtype", HIP_TYPES)
+def test_tiny_magnitudes_match_the_oracle(qs, dev, qtype):
+    """Rows scaled to ~1e-13 (their weighted error and distance terms,
+    w*d*d ~ 1e-39, are f32 subnormals), rows around the groups' activity
+    threshold (max |x| of 1e-15, GROUP_MAX_EPS) and rows of ordinary scale
+    with an imatrix of ~1e-30 (every weighted term subnormal, the blocks'
+    f16 scales representable), f32 source: the kernels keep subnormals as the
+    reference's CPU arithmetic does, and the IQ searches' choice between full
+    and reduced neighbour lists holds on terms that underflow to zero."""
+    rng = np.random.default_rng(sum(map(ord, qtype)) + 17)
+    k = 2560
+    rows = []
+    for scale in (1e-13, 3e-15, 1.2e-15, 8e-16):
+        a = rng.standard_normal((24, k)) * scale
+        rows.append(a)
+    x = np.concatenate(rows).astype(np.float32)
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    # values whose f16 block scales stay representable, with an imatrix of
+    # ~1e-30: the weights are ~1e-34 and every weighted term subnormal
+    x2 = (rng.standard_normal((32, k)) * 3e-4).astype(np.float32)
+    qw2 = (rng.lognormal(0.0, 1.0, k) * 1e-30).astype(np.float32)
+    for xs, q, what in ((x, qw, "tiny values"), (x, None, "tiny values"), (x2, qw2, "tiny imatrix")):
+        if q is None and qtype in NEEDS_IMATRIX:
+            continue
+        print(f"{qtype} imat={q is not None} {what} {xs.shape}", flush=True)
+        got = hip_quantize(qs, qtype, xs, q, dev)
+        ref = oracle.quantize(qtype, xs, None if qtype == "q4_0" else q, n_threads=NTHREADS)
+        same = block_identical(got, ref, qtype)
+        assert same.all(), f"{qtype} imat={q is not None} {what}: {int((~same).sum())}/{same.size} blocks differ"
+
+
 def test_q4_0_full_4096x4096(qs, dev):
     """Q4_0 on one bf16 4096x4096 tensor, N(0, 0.02) with 0.1%
     outliers x20, seed 0, byte-exact."""
