@@ -169,9 +169,10 @@ def test_tiny_magnitudes_match_the_oracle(qs, dev, qtype):
     w*d*d ~ 1e-39, are f32 subnormals), rows around the groups' activity
     threshold (max |x| of 1e-15, GROUP_MAX_EPS) and rows of ordinary scale
     with an imatrix of ~1e-30 (every weighted term subnormal, the blocks'
-    f16 scales representable), f32 source: the kernels keep subnormals as the
-    reference's CPU arithmetic does, and the IQ searches' choice between full
-    and reduced neighbour lists holds on terms that underflow to zero."""
+    f16 scales representable) or of ~1e34 (sums and products that overflow),
+    f32 source: the kernels keep subnormals and overflow as the reference's
+    CPU arithmetic does, and the IQ searches' choice between full and reduced
+    neighbour lists holds on terms that underflow to zero or overflow."""
     rng = np.random.default_rng(sum(map(ord, qtype)) + 17)
     k = 2560
     rows = []
@@ -184,7 +185,10 @@ def test_tiny_magnitudes_match_the_oracle(qs, dev, qtype):
     # ~1e-30: the weights are ~1e-34 and every weighted term subnormal
     x2 = (rng.standard_normal((32, k)) * 3e-4).astype(np.float32)
     qw2 = (rng.lognormal(0.0, 1.0, k) * 1e-30).astype(np.float32)
-    for xs, q, what in ((x, qw, "tiny values"), (x, None, "tiny values"), (x2, qw2, "tiny imatrix")):
+    # and an imatrix of ~1e34, whose weighted sums and products overflow to inf
+    qw3 = (rng.lognormal(0.0, 1.0, k) * 1e34).astype(np.float32)
+    for xs, q, what in ((x, qw, "tiny values"), (x, None, "tiny values"), (x2, qw2, "tiny imatrix"),
+                        (x2, qw3, "huge imatrix")):
         if q is None and qtype in NEEDS_IMATRIX:
             continue
         print(f"{qtype} imat={q is not None} {what} {xs.shape}", flush=True)
