@@ -293,6 +293,64 @@ def test_pipeline_tensors_back_to_back(tmp_path):
     assert off == len(got)
 
 
+def test_two_pipelines_on_two_threads(tmp_path):
+    """Two pipelines driven at once from two threads (each its own input
+    file, output file, copy threads, writer and streams; calls on one
+    pipeline never overlap): both outputs are the oracle's bytes."""
+    import os
+    import threading
+    qs = importlib.import_module("quant-studio_amd")
+    pl = importlib.import_module("quant-studio_amd.pipeline")
+    rng = np.random.default_rng(12)
+    jobs = []
+    for name, gts in (("a", [GT.Q4_K, GT.IQ2_XS, GT.Q6_K]), ("b", [GT.IQ3_S, GT.Q4_0, GT.IQ2_XXS])):
+        k, n = 1024, 40
+        src = tmp_path / f"{name}.bin"
+        xs = [(rng.normal(size=(n, k)) * 0.02).astype(np.float32) for _ in gts]
+        raws = [(x.view(np.uint32) >> 16).astype(np.uint16) for x in xs]
+        src.write_bytes(b"".join(r.tobytes() for r in raws))
+        qw = rng.lognormal(size=k).astype(np.float32)
+        want = [oracle.quantize(gt.name.lower(), (r.astype(np.uint32) << 16).view(np.float32),
+                                None if gt == GT.Q4_0 else qw) for gt, r in zip(gts, raws)]
+        jobs.append((name, gts, raws, qw, want, src, tmp_path / f"{name}.out"))
+    errors = []
+
+    def run(name, gts, raws, qw, want, src, out):
+        try:
+            sfd = os.open(src, os.O_RDONLY)
+            fd = os.open(out, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o644)
+            try:
+                with pl.NativePipeline(0, fd) as p:
+                    off = foff = 0
+                    for gt, raw in zip(gts, raws):
+                        info = io.TensorInfo(name, (raw.shape[1], raw.shape[0]), GT.BF16, 0, raw.nbytes,
+                                             raw.view(np.uint8).reshape(-1), foff)
+                        off += p.quantize_tensor(info, int(gt), qw, 7, off, qs.row_bytes(int(gt), raw.shape[1]),
+                                                 sfd)
+                        foff += raw.nbytes
+                    p.finish()
+            finally:
+                os.close(fd)
+                os.close(sfd)
+        except Exception as e:          # reported on the main thread
+            errors.append(f"{name}: {e}")
+
+    threads = [threading.Thread(target=run, args=j) for j in jobs]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads), "a pipeline thread did not finish"
+    assert not errors, errors
+    for name, gts, raws, qw, want, src, out in jobs:
+        got, off = out.read_bytes(), 0
+        for gt, ref in zip(gts, want):
+            part = np.frombuffer(got[off:off + ref.nbytes], np.uint8).reshape(ref.shape)
+            assert np.array_equal(part, ref), (name, gt.name)
+            off += ref.nbytes
+        assert off == len(got)
+
+
 def test_pipeline_made_on_another_thread(tmp_path):
     """PipelineStart: a pipeline created on its own thread works when taken on
     this one (the oracle's bytes), can be taken only once, and one that is
