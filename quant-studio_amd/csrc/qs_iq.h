@@ -154,8 +154,8 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 //   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
 //   res:  LDS, 64 keys
 //
-// PRUNE: the search of subgroup s (weights wv, scale sc: the very operands
-// of its distance terms) reads the code's reduced list when the code's level
+// PRUNE: the search of subgroup s (scale sc, the very operand of its
+// distance terms) reads the code's reduced list when the code's level
 // is a best level in each of its values (no level's term below its term). A
 // term is t(v) = (w*d)*d with d = sc*v - x, computed in f32. For a finite
 // w >= 0 it is a non-decreasing function of |d| (rounding is monotone and
@@ -163,21 +163,18 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // level's |d| is strictly below both neighbouring levels' (the grid's levels
 // are 0..3 for IQ2 and 0..7 for IQ3; at an end the missing neighbour is not
 // needed), d changes sign there, every other level's |d| is at least the
-// code level's, and so is its term: PRUNE 1 checks |d| alone, two
-// instructions a level instead of four (IQ2_XS and IQ3 3-5% faster), after
-// the weight is finite and >= 0. PRUNE 2 (the IQ2_XXS search, whose kernel
-// spilled twice as much with the |d| form and ran 37% slower) compares the
-// terms themselves: the code's level is a best level when its term is 0 or
-// strictly below both neighbours' (a strictly smaller term means a strictly
-// smaller |d|); where that fails only in values at the clamped top level 2
-// (IQ2) whose level-3 term is strictly below the level-2 term (so d < 0 at
-// level 2 and levels 0 and 1 have terms no smaller), the clamp-tolerant
-// reduced list is read. A negative, infinite or NaN weight or term, a NaN or
+// code level's, and so is its term: the check takes two instructions a
+// level instead of the four a term takes. The weights are square roots
+// (>= 0, or NaN); an infinite or NaN weight makes every candidate's distance
+// non-finite (each sums every value's term), so neither list has a first
+// minimum and the result is the same. With PRUNE 2, where the check fails
+// only in values at the clamped top level 2 (IQ2) whose level-3 |d| is
+// strictly below the level-2 |d| (so d < 0 at level 2 and levels 0 and 1
+// have terms no smaller), the clamp-tolerant reduced list is read. A NaN or
 // infinite d at the code level, a tie or sc <= 0 reads the full list.
 // PRUNE 0 reads the full lists.
 template <int BITS, int NV, int NSUB, int PRUNE = 0, int N>
-QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB],
-                     const float (&wv)[N], float sc) {
+QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB], float sc) {
     // all subgroups' codes first, so their cinfo loads are in flight together
     constexpr float LMAX = BITS == 2 ? 2.0f : 7.0f;
     constexpr float GMAX = BITS == 2 ? 3.0f : 7.0f;     // the grid's largest level
@@ -203,27 +200,20 @@ QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_
             const float lf = clampf(rintf(t), 0.0f, LMAX);
             code[s] |= (int)lf << (BITS * j);
             if constexpr (PRUNE > 0) {
-                const float v = 2.0f * lf + 1.0f, w = wv[NV * s + j];
+                const float v = 2.0f * lf + 1.0f;
+                auto dist = [&](float lv) {
+                    float d = sc * lv;
+                    d = d - x;
+                    return fabsf(d);
+                };
+                const float du = dist(v), dm = dist(v - 2.0f), dp = dist(v + 2.0f);
+                const bool ok = (lf == 0.0f || du < dm) && (lf == GMAX || du < dp);
                 if constexpr (PRUNE == 2) {
-                    auto term = [&](float lv) {
-                        float d = sc * lv;
-                        d = d - x;
-                        return (w * d) * d;
-                    };
-                    const float tu = term(v), tm = term(v - 2.0f), tp = term(v + 2.0f);
-                    const bool ok = tu == 0.0f || ((lf == 0.0f || tu < tm) && (lf == GMAX || tu < tp));
-                    // the clamped top level with the grid's level 3 strictly better
-                    const bool up = LMAX < GMAX && lf == LMAX && tp < tu;
+                    // the clamped top level with the grid's level 3 strictly closer
+                    const bool up = LMAX < GMAX && lf == LMAX && dp < du;
                     miss[s] |= ok ? 0 : up ? 1 : 3;
                 } else {
-                    auto dist = [&](float lv) {
-                        float d = sc * lv;
-                        d = d - x;
-                        return fabsf(d);
-                    };
-                    const float du = dist(v), dm = dist(v - 2.0f), dp = dist(v + 2.0f);
-                    const bool wfin = w >= 0.0f && w <= __FLT_MAX__;
-                    best[s] = best[s] && wfin && (lf == 0.0f || du < dm) && (lf == GMAX || du < dp);
+                    best[s] = best[s] && ok;
                 }
             }
         }
@@ -553,7 +543,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gi[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, waux, sc);
+        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, sc);
         static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
@@ -573,7 +563,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         int gp[4];
         bool on;
         uint32_t ci[4];
-        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, waux, scale);
+        iq_codes<2, 8, 4, 2>(T, xval, inv, ci, scale);
         static_for<0, 4>([&](auto S) {
             gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
@@ -675,7 +665,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         int gi[2];
         bool on[2];
         uint32_t ci[2];
-        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, waux, sc);
+        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, sc);
         gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
         gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
         float sumqx, sumq2;
@@ -697,7 +687,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         const float inv = 1.0f / (need ? scale : 1.0f);
         bool on;
         uint32_t ci[2];
-        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, waux, scale);
+        iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, scale);
         const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
                                                           need && !og[0], on);
         const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
@@ -840,7 +830,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int gi[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL, 1>(T, xval, inv, ci, waux, sc);
+        iq_codes<3, 4, NSL, 1>(T, xval, inv, ci, sc);
         static_for<0, NSL>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
@@ -868,7 +858,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         int w2[NSL];
         bool on[NSL];
         uint32_t ci[NSL];
-        iq_codes<3, 4, NSL, 1>(T, xval, inv2, ci, waux, scale);
+        iq_codes<3, 4, NSL, 1>(T, xval, inv2, ci, scale);
         static_for<0, NSL>([&](auto S) {
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);
