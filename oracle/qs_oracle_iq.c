@@ -96,13 +96,16 @@ static inline float grid_val(const IqTab *T, int gi, int j) {
     return (float)(2 * ((T->grid[gi] >> (T->bits * j)) & ((1 << T->bits) - 1)) + 1);
 }
 
-/* Best neighbour of an off-grid code: first minimum of the weighted squared
- * distance. IQ2 (8 values): d2 is torch's `.sum(-1)` of 8 terms, a left-to-
- * right sum from +0 (iq2.py:366-369, iq2xs_common.py:236-240); IQ3 (4 values):
- * ((t0+t1)+t2)+t3 (iq3_common.py:229-233). t = (wv*diff)*diff, diff = sc*g - x. */
+/* Best neighbour of an off-grid code: torch's d2.argmin(-1) over the list
+ * (iq2.py:366-371, iq2xs_common.py:236-241, iq3_common.py:228-235), the first
+ * NaN distance if there is one, else the first minimum (the first entry when
+ * every distance is +inf). IQ2 (8 values): d2 is torch's `.sum(-1)` of 8
+ * terms, a left-to-right sum from +0 (iq2.py:366-369, iq2xs_common.py:236-240);
+ * IQ3 (4 values): ((t0+t1)+t2)+t3 (iq3_common.py:229-233).
+ * t = (wv*diff)*diff, diff = sc*g - x. */
 static int nearest(const IqTab *T, int code, const float *xv, const float *wv, float sc) {
     const int n = T->nsub;
-    float best = INFINITY;
+    float best = 0.0f;
     int besti = -1;
     for (int k = 0; k < T->nlen[code]; k++) {
         int gi = T->nbr[T->nstart[code] + k];
@@ -113,7 +116,8 @@ static int nearest(const IqTab *T, int code, const float *xv, const float *wv, f
             float t = (wv[j] * diff) * diff;
             d2 = (n == 4 && j == 0) ? t : d2 + t;
         }
-        if (d2 < best || (g_mut == MUT_IQ_LAST_MIN && d2 == best)) { best = d2; besti = gi; }
+        if (isnan(d2)) return gi;
+        if (besti < 0 || d2 < best || (g_mut == MUT_IQ_LAST_MIN && d2 == best)) { best = d2; besti = gi; }
     }
     return besti;
 }

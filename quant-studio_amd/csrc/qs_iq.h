@@ -137,10 +137,11 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // Project every lane's subgroups at its candidate scale
 // (iq2.py:347-372, iq2xs_common.py:222-271, iq3_common.py:209-256): levels
 // clamp(round(0.5*(inv*x - 1)), 0, LMAX) -> code -> kmap hit (iq_codes), or
-// the first minimum of the weighted distance over the code's neighbour list
-// (iq_search, one call per subgroup OFF..OFF+NV-1). IQ2
-// distances are a left-to-right sum of 8 terms from +0; IQ3's are
-// ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and diff = sc*g - x.
+// the reference's d2.argmin(-1) over the code's neighbour list (iq_search,
+// one call per subgroup OFF..OFF+NV-1). IQ2 distances are a left-to-right sum
+// of 8 terms from +0; IQ3's are ((t0+t1)+t2)+t3, with t = (wv*diff)*diff and
+// diff = sc*g - x. torch's argmin takes the first NaN as the minimum, else
+// the first minimum (the first entry when every distance is +inf).
 //
 // The search is wave-balanced: the off-grid lanes' lists are cut into chunks
 // of CH candidates and the wave's chunks are dealt to all 64 lanes in turn, so
@@ -148,11 +149,23 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // owner's values and scale with ds_bpermute, evaluates its candidates in list
 // order and merges its first minimum into the owner's LDS slot as a 64-bit key
 // (distance bits, list position, grid index); the least key is the list's
-// first minimum, the result of the reference's sequential scan. Every lane of
-// the wave calls this together; lanes with want == false take part but search
-// nothing (their result is unused).
+// first finite minimum. Every lane of the wave calls this together; lanes
+// with want == false take part but search nothing (their result is grid
+// index 0 and unused).
 //   cmap: LDS, 64 * MAXCH bytes (chunk -> owner lane)
 //   res:  LDS, 64 keys
+//
+// NaN terms. A term is NaN only for a NaN weight or value, for w = +inf at
+// d = 0, or for w = +-0 at an infinite d. With the reference's weights
+// (qw*sqrt(sigma2 + x^2), or x^2 without an imatrix) a NaN distance never sits
+// next to a finite one: an infinite d needs |x| or sc (at most about max |x|)
+// near 1e37, where x^2 and sigma2 overflow, so every searched subgroup then
+// holds a +inf or NaN weight (a subgroup off the all-zero code has a value at
+// level >= 1, within a factor ~10 of max |x|); and a +inf or NaN weight makes
+// that value's term +inf or NaN for every candidate. So when no distance is
+// finite, iq_search hands the list back (iq_search_miss) and iq_rescan scans
+// it in order for the first NaN, else takes the first entry; otherwise the
+// least key is the argmin.
 //
 // PRUNE: the search of subgroup s (scale sc, the very operand of its
 // distance terms) reads the code's reduced list when the code's level
@@ -165,14 +178,17 @@ QS_DEV float level(const Levels<NV>& L, int e) {
 // needed), d changes sign there, every other level's |d| is at least the
 // code level's, and so is its term: the check takes two instructions a
 // level instead of the four a term takes. The weights are square roots
-// (>= 0, or NaN); an infinite or NaN weight makes every candidate's distance
-// non-finite (each sums every value's term), so neither list has a first
-// minimum and the result is the same. With PRUNE 2, where the check fails
-// only in values at the clamped top level 2 (IQ2) whose level-3 |d| is
-// strictly below the level-2 |d| (so d < 0 at level 2 and levels 0 and 1
-// have terms no smaller), the clamp-tolerant reduced list is read. A NaN or
-// infinite d at the code level, a tie or sc <= 0 reads the full list.
-// PRUNE 0 reads the full lists.
+// (>= 0, -0 or NaN). A NaN weight makes every distance NaN (the first entry
+// wins, and no reduced list leaves it out); at a +inf weight only the code's
+// level can have d = 0, so an entry left out for an earlier one that keeps
+// every level it keeps is NaN only when that earlier one is: the first NaN
+// and the first entry are the same in either list. With PRUNE 2, where the
+// check fails only in values at the clamped top level 2 (IQ2) whose level-3
+// |d| is strictly below the level-2 |d| (so d < 0 at level 2 and levels 0 and
+// 1 have terms no smaller), the clamp-tolerant reduced list is read (an entry
+// it leaves out also shares every raise to level 3 with the earlier one). A
+// NaN or infinite d at the code level, a tie or sc <= 0 reads the full
+// list. PRUNE 0 reads the full lists.
 template <int BITS, int NV, int NSUB, int PRUNE = 0, int N>
 QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_t (&ci)[NSUB], float sc) {
     // all subgroups' codes first, so their cinfo loads are in flight together
@@ -226,13 +242,44 @@ QS_DEV void iq_codes(const IqTabDev& T, const float (&xv)[N], float inv, uint32_
     }
 }
 
+// torch's argmin over one neighbour list, entry by entry, with the distance
+// arithmetic of iq_chunk_best: the first NaN distance, else the first
+// minimum (the list's first entry when every distance is +inf).
+template <int NV, int CH>
+QS_DEV int iq_argmin_scan(const IqTabDev& T, const uint32_t* glds, uint32_t ci, const float (&xs)[NV],
+                          const float (&ws)[NV], float sc) {
+    const uint16_t* list = T.nbr + (size_t)((ci >> 12) & 0x7ffffu) * CH;
+    const int n = (int)(ci & 0xfffu);
+    int best_gi = list[0];
+    float best = 0.0f;
+    for (int k = 0; k < n; k++) {
+        const int gi = list[k];
+        const Levels<NV> gl = grid_levels<NV>(glds, gi);
+        float d2 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NV; e++) {
+            float diff = sc * level<NV>(gl, e);
+            diff = diff - xs[e];
+            const float t = (ws[e] * diff) * diff;
+            d2 = (e == 0) ? t : d2 + t;
+        }
+        if (d2 != d2) return gi;
+        if (k == 0 || d2 < best) {
+            best = d2;
+            best_gi = gi;
+        }
+    }
+    return best_gi;
+}
+
 // First minimum of one chunk (CH list slots from slot CH*kc) as a 64-bit key
 // (distance bits, list position, grid index); slots past the list end (o_n)
 // are masked out. Every slot is evaluated (padding holds index 0, a valid
 // grid point), without branches. IQ2: slots are visited in list order, so a
 // strict `d2 < best` keeps the first minimum and the key is built once per
 // chunk (4-7% faster); a chunk with no finite distance returns ~0 (as if it
-// held no candidate: the search's result is then -1 either way). IQ3 compares
+// held no candidate: with no finite distance anywhere in the list the search
+// hands the list to iq_rescan either way). IQ3 compares
 // the 64-bit key per slot (its 4-slot chunks measured 1-2% faster that way).
 template <int BITS, int NV, int CH>
 QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&wd)[CH / 2], int kc, int o_n,
@@ -258,8 +305,9 @@ QS_DEV unsigned long long iq_chunk_best(const uint32_t* glds, const uint32_t (&w
             float diff = o_sc * level<NV>(gl[j], e);
             diff = diff - xs[e];
             // IQ2's sum runs from +0 (iq2.py) and IQ3's from its first term;
-            // t = (w*d)*d is never -0 (the two factors d carry the same
-            // sign), so +0 + t0 == t0 and both start from the first term
+            // t = (w*d)*d is -0 only for w = -0, and a subgroup whose weights
+            // are all -0 has -0 (or NaN) for every candidate, so starting
+            // from the first term decides no different minimum
             const float t = (ws[e] * diff) * diff;
             d2 = (e == 0) ? t : d2 + t;
         }
@@ -292,6 +340,10 @@ QS_DEV void iq_load_chunk(const IqTabDev& T, size_t chunk, uint32_t (&wd)[CH / 2
         wd[0] = q.x; wd[1] = q.y;
     }
 }
+
+// The result of a search with no finite distance: its list's cinfo word
+// (off-grid, so bit 31 is free) with bit 31 set, a negative int.
+QS_DEV int iq_search_miss(uint32_t ci) { return (int)(ci | CI_ON_GRID); }
 
 template <int BITS, int NV, int OFF, int CH, int MAXCH, bool WL = false, int N>
 QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, unsigned long long* res,
@@ -357,8 +409,33 @@ QS_DEV int iq_search(const IqTabDev& T, const uint32_t* glds, uint8_t* cmap, uns
     if (on) return (int)(ci & 0xffffu);
     const unsigned long long r0 = res[lane];
     const unsigned long long r = r0 < best_own ? r0 : best_own;
-    // no finite distance: the sequential scan keeps its initial -1
-    return (uint32_t)(r >> 32) >= 0x7f800000u ? -1 : (int)(r & 0xffffu);
+    // a finite first minimum (-0, every distance of a subgroup whose weights
+    // are all -0, counts as one), else the list for iq_rescan
+    const bool fin = ((uint32_t)(r >> 32) & 0x7fffffffu) < 0x7f800000u;
+    return n == 0 ? 0 : fin ? (int)(r & 0xffffu) : iq_search_miss(ci);
+}
+
+// Every subgroup whose search found no finite distance (rare: an infinite
+// or NaN weight, value or scale) gets torch's argmin from an in-order scan
+// of its list; the wave skips this when none did.
+template <int NV, int CH, int NSUB, int N>
+QS_DEV void iq_rescan(const IqTabDev& T, const uint32_t* glds, const float (&xv)[N], const float (&wv)[N],
+                      float sc, int (&gi)[NSUB]) {
+    bool miss = false;
+#pragma unroll
+    for (int s = 0; s < NSUB; s++) miss = miss || gi[s] < 0;
+    if (!wave_any(miss)) return;
+    static_for<0, NSUB>([&](auto S) {
+        if (gi[S] < 0) {
+            float xs[NV], ws[NV];
+#pragma unroll
+            for (int e = 0; e < NV; e++) {
+                xs[e] = xv[NV * S + e];
+                ws[e] = wv[NV * S + e];
+            }
+            gi[S] = iq_argmin_scan<NV, CH>(T, glds, (uint32_t)gi[S] & ~CI_ON_GRID, xs, ws, sc);
+        }
+    });
 }
 
 // sign-parity fold of 8 values (iq2.py:438-450): |x|, the smallest (w*x)*x
@@ -547,6 +624,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         static_for<0, 4>([&](auto S) {
             gi[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on);
         });
+        iq_rescan<8, IQ2_CH>(T, glds, xval, waux, sc, gi);
         float sumqx, sumq2;
         iq_cascade_sums_32(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -567,6 +645,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3))) void k_
         static_for<0, 4>([&](auto S) {
             gp[S] = iq_search<2, 8, 8 * S, IQ2_CH, IQ2_256_MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S], proj, on);
         });
+        iq_rescan<8, IQ2_CH>(T, glds, xval, waux, scale, gp);
         float sumqx, sumq2;
         iq_cascade_sums_32(glds, gp, w, xval, sumqx, sumq2);
         if (proj && sumq2 > 0) scale = sumqx / fmaxf(sumq2, F32_TINY);
@@ -668,6 +747,7 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, sc);
         gi[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[0], true, on[0]);
         gi[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, sc, ci[1], true, on[1]);
+        iq_rescan<8, IQ2_CH>(T, glds, xval, waux, sc, gi);
         float sumqx, sumq2;
         iq_tree_sums<2, 8, 2>(glds, gi, w, xval, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -688,12 +768,14 @@ __global__ __launch_bounds__(64 * WPG) __attribute__((amdgpu_waves_per_eu(IS_S &
         bool on;
         uint32_t ci[2];
         iq_codes<2, 8, 2, IS_S ? 0 : 1>(T, xval, inv, ci, scale);
-        const int r0 = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
-                                                          need && !og[0], on);
-        const int r1 = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
-                                                          need && !og[1], on);
-        if (need && !og[0]) win[0] = r0;
-        if (need && !og[1]) win[1] = r1;
+        int r[2];
+        r[0] = iq_search<2, 8, 0, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[0],
+                                                     need && !og[0], on);
+        r[1] = iq_search<2, 8, 8, IQ2_CH, MAXCH, WL>(T, glds, cmap, res, xval, waux, scale, ci[1],
+                                                     need && !og[1], on);
+        iq_rescan<8, IQ2_CH>(T, glds, xval, waux, scale, r);
+        if (need && !og[0]) win[0] = r[0];
+        if (need && !og[1]) win[1] = r[1];
     }
     if (need) {
         float sumqx, sumq2;
@@ -834,6 +916,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
         static_for<0, NSL>([&](auto S) {
             gi[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, sc, ci[S], true, on[S]);
         });
+        iq_rescan<4, IQ3_CH>(T, glds, xval, waux, sc, gi);
         float sumqx, sumq2;
         group_sums(gi, sumqx, sumq2);
         if (active && sumq2 > 0 && sumqx * sumqx > best * sumq2) {
@@ -863,6 +946,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(LPG == 4 ? 6
             w2[S] = iq_search<3, 4, 4 * S, IQ3_CH, MAXCH>(T, glds, cmap, res, xval, waux, scale, ci[S],
                                                           redo && (IS_S || !og[S]), on[S]);
         });
+        iq_rescan<4, IQ3_CH>(T, glds, xval, waux, scale, w2);
 #pragma unroll
         for (int k = 0; k < NSL; k++)
             if (redo && (IS_S || !og[k])) Wg[k] = w2[k];

@@ -198,6 +198,62 @@ def test_tiny_magnitudes_match_the_oracle(qs, dev, qtype):
         assert same.all(), f"{qtype} imat={q is not None} {what}: {int((~same).sum())}/{same.size} blocks differ"
 
 
+def nan_sign_cleared(b: np.ndarray, nb: int) -> np.ndarray:
+    """Blocks with the sign bit of a NaN f16 block scale (bytes 0-1) cleared."""
+    b = b.reshape(-1, nb).copy()
+    d = b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8)
+    nan = ((d & 0x7C00) == 0x7C00) & ((d & 0x03FF) != 0)
+    b[nan, 1] &= 0x7F
+    return b
+
+
+@pytest.mark.parametrize("qtype", HIP_TYPES)
+def test_special_weights_and_near_max_values(qs, dev, qtype):
+    """Imatrix columns of +inf, NaN and -0 (whole superblocks, a 32-value
+    group, a 4-value subgroup), and rows holding values near FLT_MAX next to
+    zeros, f32 source. An IQ search whose distances are all +inf or NaN takes
+    the list's first NaN, else its first entry, as torch's argmin does
+    (iq2.py:366-371, iq3_common.py:228-235); -0 weights give -0 distances,
+    which tie; values near FLT_MAX overflow x^2 and the superblock's sigma2,
+    so their weights are +inf (or NaN at a zero importance). The GPU
+    returns the oracle's bytes on every block (IQ4_XS and IQ3_S up to the sign
+    of a NaN block scale, positive on the GPU and negative on x86)."""
+    rng = np.random.default_rng(sum(map(ord, qtype)) + 29)
+    k, nb = 2560, TYPES[qtype][2]
+    x = (rng.standard_normal((64, k)) * 0.02).astype(np.float32)
+    runs = []
+    for what, val in (("+inf columns", np.inf), ("NaN columns", np.nan)):
+        qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+        qw[rng.choice(k, 6, replace=False)] = val
+        runs.append((what, x, qw))
+    qw = rng.lognormal(0.0, 1.0, k).astype(np.float32)
+    qw[256:512] = -0.0
+    qw[1024:1056] = -0.0
+    qw[2000:2004] = -0.0
+    runs.append(("-0 columns", x, qw))
+    xb = x.copy()
+    xb[0:16, 5] = 3.0e38                 # one value near FLT_MAX, the rest of its group zero
+    xb[0:16, 0:5] = 0.0
+    xb[0:16, 6:32] = 0.0
+    xb[16:32, 300] = -2.9e38
+    xb[16:32, 288:300] = 0.0
+    xb[32:48, 600] = 2.0e36              # beyond 2^120: full lists, no overflow
+    xb[48:64, 1000:1004] = 0.0
+    xb[48:64, 1004] = 3.3e38
+    runs.append(("near-max values", xb, None))
+    runs.append(("near-max values", xb, rng.lognormal(0.0, 1.0, k).astype(np.float32)))
+    for what, xs, q in runs:
+        if q is None and qtype in NEEDS_IMATRIX:
+            continue
+        print(f"{qtype} imat={q is not None} {what}", flush=True)
+        got = hip_quantize(qs, qtype, xs, q, dev)
+        ref = oracle.quantize(qtype, xs, None if qtype == "q4_0" else q, n_threads=NTHREADS)
+        if qtype in NAN_SIGN_TYPES:
+            got, ref = nan_sign_cleared(got, nb), nan_sign_cleared(ref, nb)
+        same = (got.reshape(-1, nb) == ref.reshape(-1, nb)).all(1)
+        assert same.all(), f"{qtype} imat={q is not None} {what}: {int((~same).sum())}/{same.size} blocks differ"
+
+
 def test_q4_0_full_4096x4096(qs, dev):
     """Q4_0 on one bf16 4096x4096 tensor, N(0, 0.02) with 0.1%
     outliers x20, seed 0, byte-exact."""
